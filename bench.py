@@ -1,0 +1,249 @@
+"""Benchmark of the fused FFN on one MI355X: fused FFN TFLOP/s and fraction of MFMA peak,
+Basic vs Stream-K down-projection.
+
+A step is one PreparedFFN.run() (up GEMM + GELU epilogue, then the down GEMM) over
+one batch of seeded synthetic input already resident in HBM.  The headline
+workload is the aligned mid-size FFN (X [4096,1024] bf16, W1 [4096,1024],
+W2 [1024,4096]); the other workloads are reported beside it.  Timing mirrors
+performance/collect.py:8-35 of the reference (warmup, then device events).
+
+Prints ONE JSON line.  --gpus above 1 is refused: this operator runs on one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+if str(REPO) not in sys.path:
+    sys.path.insert(0, str(REPO))
+
+METRIC = "fused FFN TFLOP/s (4·M·K·H-equiv FLOPs) and % of MFMA peak, Basic vs Stream-K"
+MFMA_PEAK_TFLOPS = 2500.0   # MI355X dense FP16/BF16 MFMA, published
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, published
+HEADLINE = "c2_aligned_bf16"
+EXTRA = ("c5_dit_bf16", "c4_decode_bf16", "c3_unaligned_fp16", "c1_smoke_fp16")
+
+
+def parse_args(argv=None):
+    p = argparse.ArgumentParser(description=__doc__)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--case", default=HEADLINE)
+    p.add_argument("--no-extra", action="store_true", help="headline workload only")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU oracle time budget")
+    return p.parse_args(argv)
+
+
+def workload_numbers(case):
+    from ffn_optim_amd.cases import case_problem
+    p = case_problem(case)
+    m, k, h, n = p.m, p.k, p.h, p.n
+    esz = 2
+    return {
+        "m": m, "k": k, "h": h, "n": n,
+        "flops_4mkh": 4.0 * m * k * h,
+        "flops": 2.0 * m * h * (k + n),
+        "flops_up": 2.0 * m * k * h,
+        "flops_down": 2.0 * m * h * n,
+        "bytes": float(esz * (m * k + h * k + n * h + m * n)),
+        "bytes_up": float(esz * (m * k + h * k + m * h)),
+        "bytes_down": float(esz * (m * h + n * h + m * n)),
+    }
+
+
+def time_events(fn, steps, warmup, stream=None, flush=None):
+    """Median and mean per-call device time (ms) with events on the current stream."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if flush is None:
+        start.record()
+        for _ in range(steps):
+            fn()
+        end.record()
+        end.synchronize()
+        total = start.elapsed_time(end)
+        return {"mean_ms": total / steps, "total_ms": total}
+    samples = []
+    for _ in range(steps):
+        flush()
+        start.record()
+        fn()
+        end.record()
+        end.synchronize()
+        samples.append(start.elapsed_time(end))
+    return {"mean_ms": statistics.fmean(samples), "median_ms": statistics.median(samples),
+            "total_ms": sum(samples)}
+
+
+def measure_path(case, down, steps, warmup, inputs):
+    """Time whole steps, then the up and down kernels alone, for one down implementation."""
+    import ctypes
+    import torch
+    from ffn_optim_amd import _lib, prepare_ffn
+    x, w1, w2 = inputs
+    prepared = prepare_ffn(x, w1, w2, down_impl=down)
+    lib = _lib.load()
+    plan = prepared.plan.native
+    xs, w1s, w2s, hid, out, ws = prepared.tensors
+    stream = torch.cuda.current_stream().cuda_stream
+
+    torch.cuda.synchronize()
+    step = time_events(prepared.run, steps, warmup)
+
+    def up():
+        lib.ffn_mi355x_up(ctypes.byref(plan), xs, w1s, hid, stream)
+
+    def dn():
+        lib.ffn_mi355x_down(ctypes.byref(plan), hid, w2s, out, ws, stream)
+
+    t_up = time_events(up, steps, warmup)
+    t_dn = time_events(dn, steps, warmup)
+    return prepared, step, t_up, t_dn
+
+
+def traffic_from_profiles(kernel_tag, case_id):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by a
+    copy-kernel calibration), read from the committed summary if one exists."""
+    path = REPO / "profiles" / f"traffic_{kernel_tag}_{case_id}.md"
+    if not path.exists():
+        return None
+    m = re.search(r"^hbm_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text(), re.M)
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(case, budget_s):
+    """The oracle's torch FP32 path (validation/reference.py:16-23) on this host's cores."""
+    import torch
+    from ffn_optim_amd.cases import make_inputs
+    from oracle.reference import ffn_torch
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    x, w1, w2 = make_inputs(case, "cpu")
+    nums = workload_numbers(case)
+    ffn_torch(x, w1, w2)  # warmup
+    samples = []
+    t_end = time.perf_counter() + budget_s
+    while len(samples) < 3 or (time.perf_counter() < t_end and len(samples) < 50):
+        t0 = time.perf_counter()
+        ffn_torch(x, w1, w2)
+        samples.append(time.perf_counter() - t0)
+    med = statistics.median(samples)
+    cpu = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": nums["flops_4mkh"] / med / 1e12, "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{len(samples)} full runs of {case['case_id']} (median {med*1e3:.1f} ms, "
+                      f"{sum(samples):.1f} s total) with torch FP32 on {threads} threads, {cpu}"}
+
+
+def bench_case(case, steps, warmup):
+    import torch
+    from ffn_optim_amd.cases import make_inputs
+    nums = workload_numbers(case)
+    inputs = make_inputs(case, "cuda")
+    res = {}
+    for down in ("basic", "streamk"):
+        try:
+            prepared, step, t_up, t_dn = measure_path(case, down, steps, warmup, inputs)
+        except ValueError as exc:
+            res[down] = {"status": "not_applicable", "reason": str(exc)}
+            continue
+        ms = step["mean_ms"]
+        res[down] = {
+            "ms_per_step": ms,
+            "tflops_4mkh": nums["flops_4mkh"] / ms / 1e9,
+            "mfma_peak_frac": nums["flops_4mkh"] / ms / 1e9 / MFMA_PEAK_TFLOPS,
+            "hbm_gbs": nums["bytes"] / ms / 1e6,
+            "up_ms": t_up["mean_ms"], "down_ms": t_dn["mean_ms"],
+            "up_tflops": nums["flops_up"] / t_up["mean_ms"] / 1e9,
+            "down_tflops": nums["flops_down"] / t_dn["mean_ms"] / 1e9,
+            "up_tile": [prepared.plan.up.bm, prepared.plan.up.bn, prepared.plan.up.bk],
+            "down_tile": [prepared.plan.down.bm, prepared.plan.down.bn, prepared.plan.down.bk],
+            "block_num": prepared.plan.block_num,
+        }
+        del prepared
+    torch.cuda.synchronize()
+    return nums, res
+
+
+def main(argv=None):
+    args = parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py: this operator runs on one GPU; --gpus {args.gpus} is not supported "
+              "(multi-GPU sharding is design-only)", file=sys.stderr)
+        return 2
+    import torch
+    from ffn_optim_amd.cases import get_case
+
+    case = get_case(args.case)
+    nums, res = bench_case(case, args.steps, args.warmup)
+    paths = {k: v for k, v in res.items() if "ms_per_step" in v}
+    if not paths:
+        raise RuntimeError(f"no runnable path for {args.case}: {res}")
+    best_down = min(paths, key=lambda k: paths[k]["ms_per_step"])
+    best = paths[best_down]
+    # dominant kernel of the best path
+    if best["up_ms"] >= best["down_ms"]:
+        kname, kms, kflops, ktag = "up GEMM + GELU", best["up_ms"], nums["flops_up"], "up"
+    else:
+        kname, kms, kflops, ktag = f"down GEMM ({best_down})", best["down_ms"], nums["flops_down"], f"down_{best_down}"
+    achieved = kflops / kms / 1e9
+    roofline = {"bound": "mfma", "achieved": achieved, "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": achieved / MFMA_PEAK_TFLOPS,
+                "traffic": traffic_from_profiles(ktag, args.case),
+                "kernel": kname, "kernel_ms": kms, "algorithmic_flops_per_launch": kflops}
+    workloads = {}
+    if not args.no_extra:
+        for cid in EXTRA:
+            if cid == args.case:
+                continue
+            c = get_case(cid)
+            wn, wr = bench_case(c, max(10, args.steps // 2), args.warmup)
+            workloads[cid] = {"flops_4mkh": wn["flops_4mkh"], "alg_bytes": wn["bytes"], **wr}
+    line = {
+        "metric": METRIC,
+        "value": best["tflops_4mkh"],
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": best["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if case["dtype"] == "bfloat16" else "fp16",
+        "data": "synthetic: seeded randn, X ~ N(0,1), W1 ~ N(0,1/K), W2 ~ N(0,1/H)",
+        "config": {"workload": f"{args.case}: X{case['shape']} W1{case['weight1_shape']} "
+                               f"W2{case['weight2_shape']}",
+                   "down_impl": best_down, "block_num": best["block_num"],
+                   "mfma_peak_frac": best["mfma_peak_frac"]},
+        "roofline": roofline,
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(case, args.cpu_seconds),
+        "paths": res,
+        "workloads": workloads,
+        "device": torch.cuda.get_device_name(0),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -1,0 +1,117 @@
+"""ctypes binding of ``libffn_mi355x.so`` (declarations in include/ffn_mi355x.h).
+
+Loading the library touches no GPU; only the run entry points and
+``ffn_mi355x_query`` talk to the HIP runtime.  Return codes are mapped onto the
+reference's exception taxonomy (ops/api.py:9-14, ops/host/dispatch.py:22-39).
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIBRARY_PATH = Path(__file__).resolve().parent / "libffn_mi355x.so"
+
+FP16, BF16 = 0, 1
+DOWN_CODES = {"basic": 0, "streamk": 1, "full_load_a": 2, "full_load_b": 3}
+GELU_CODES = {"erf": 0, "rational": 1}
+
+OK, EINVAL, ENOT_APPLICABLE, EUNAVAILABLE, EHIP, EDEVICE = 0, -1, -2, -3, -4, -5
+
+
+class PlanStruct(ctypes.Structure):
+    """Mirror of ``ffn_mi355x_plan``."""
+
+    _fields_ = [(name, ctypes.c_int) for name in (
+        "mp", "kp", "hp", "np", "dtype", "down_impl", "gelu", "block_num",
+        "up_variant", "down_variant", "up_bm", "up_bn", "up_bk",
+        "down_bm", "down_bn", "down_bk", "up_tiles", "up_grid",
+        "down_tiles", "down_grid", "down_k_iters", "down_dp_tiles",
+        "down_sk_tiles", "down_slots_per_wg")] + [("workspace_bytes", ctypes.c_size_t)]
+
+    def to_dict(self):
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+_P = ctypes.POINTER
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+SIGNATURES = {
+    "ffn_mi355x_query": (_i, [_i, _P(_i), ctypes.c_char_p, _i]),
+    "ffn_mi355x_make_plan": (_i, [_i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _P(PlanStruct)]),
+    "ffn_mi355x_workspace_bytes": (_i, [_P(PlanStruct), _P(ctypes.c_size_t)]),
+    "ffn_mi355x_run": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ffn_mi355x_up": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp]),
+    "ffn_mi355x_down": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp]),
+    "ffn_mi355x_num_variants": (_i, []),
+    "ffn_mi355x_variant_info": (_i, [_i, _P(_i), _P(_i), _P(_i), _P(_i), _P(_i), _P(_i)]),
+    "ffn_mi355x_last_error": (ctypes.c_char_p, []),
+    "ffn_mi355x_strerror": (ctypes.c_char_p, [_i]),
+    "ffn_mi355x_version": (ctypes.c_char_p, []),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load(path: Path | str | None = None):
+    """Load (once) and return the library; raises OSError if it cannot be loaded."""
+    global _lib
+    with _lock:
+        if _lib is None or path is not None:
+            lib = ctypes.CDLL(str(path or LIBRARY_PATH), mode=ctypes.RTLD_LOCAL)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype, fn.argtypes = res, args
+            if path is not None:
+                return lib
+            _lib = lib
+        return _lib
+
+
+def last_error() -> str:
+    return load().ffn_mi355x_last_error().decode()
+
+
+def check(rc: int) -> None:
+    """Raise the reference-equivalent exception for a non-zero return code."""
+    if rc == OK:
+        return
+    from .host.dispatch import DependencyUnavailable, NotApplicable
+    msg = last_error() or load().ffn_mi355x_strerror(rc).decode()
+    if rc == EINVAL:
+        raise ValueError(msg)
+    if rc == ENOT_APPLICABLE:
+        raise NotApplicable(msg)
+    if rc == EUNAVAILABLE:
+        raise DependencyUnavailable(msg)
+    raise RuntimeError(msg)
+
+
+def query(device: int) -> tuple[int, str]:
+    """(CU count, gcnArchName) of a device; RuntimeError unless it is gfx950."""
+    lib = load()
+    cus = ctypes.c_int(0)
+    arch = ctypes.create_string_buffer(64)
+    check(lib.ffn_mi355x_query(device, ctypes.byref(cus), arch, len(arch)))
+    return cus.value, arch.value.decode()
+
+
+def make_plan(mp, kp, hp, np_, dtype, down_impl, gelu, block_num, up_variant=-1,
+              down_variant=-1) -> PlanStruct:
+    plan = PlanStruct()
+    check(load().ffn_mi355x_make_plan(mp, kp, hp, np_, dtype, DOWN_CODES[down_impl],
+                                      GELU_CODES[gelu], block_num, up_variant, down_variant,
+                                      ctypes.byref(plan)))
+    return plan
+
+
+def variants() -> list[dict]:
+    lib = load()
+    out = []
+    for v in range(lib.ffn_mi355x_num_variants()):
+        vals = [ctypes.c_int(0) for _ in range(6)]
+        check(lib.ffn_mi355x_variant_info(v, *map(ctypes.byref, vals)))
+        out.append(dict(zip(("bm", "bn", "bk", "waves", "stages", "lds_bytes"),
+                            (x.value for x in vals)), variant=v))
+    return out

@@ -1,0 +1,112 @@
+"""Drop-in FFN API: ``ffn``, ``prepare_ffn``, ``PreparedFFN.run`` (restates ops/api.py).
+
+    Y = GELU(X @ weight1.T) @ weight2.T       no bias, no autograd
+
+X is 2-8-D [..., K], weight1 [H, K], weight2 [N, H], all float16 or bfloat16 on
+one ROCm GPU (gfx950).  Inputs are contiguised and zero-padded on entry (M/H/N to
+64, K to 16), the output is cropped and the leading dims restored.  Differences
+from the reference, by design of the target:
+  * block_num is the number of persistent workgroups (<= the device CU count);
+    its default None means "every CU" instead of the reference's 8 AI cores.
+  * gelu='erf' (exact GELU, the reference's golden) or 'rational' (the
+    reference's P5/Q5 kernel approximation) selects the up-projection epilogue.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from time import perf_counter
+
+from .host.dispatch import Selection, verify_dependency
+from .host.inputs import prepare_storage, validate_tensors
+from .host.tiling import make_plan
+
+
+class KernelCompilationError(RuntimeError):
+    """Loading or binding the prebuilt kernels failed (ops/api.py:9-14).
+
+    Raised before any FFN launch; input preparation may already have run.
+    The original exception is chained.
+    """
+
+
+@dataclass
+class PreparedFFN:
+    """Prepared inputs, buffers and bound kernels; run() may be called repeatedly.
+
+    storage is (X[mp,kp], W1[hp,kp], W2[np,hp], hidden[mp,hp], out[mp,np], ws) on
+    one device; tensors holds their device addresses; provenance and preparation
+    record the library and the preparation timings; stream is the preparation
+    stream (ops/api.py:17-35).
+    """
+
+    plan: object
+    storage: tuple
+    tensors: tuple
+    artifact: object
+    provenance: dict
+    preparation: dict
+    stream: object
+
+    def run(self):
+        """One FFN launch sequence; the returned view is overwritten by the next run().
+
+        Must be called on the preparation stream; returns without synchronising
+        (ops/api.py:37-45).
+        """
+        import torch
+        with torch.cuda.device(self.storage[0].device):
+            stream = torch.cuda.current_stream()
+            if stream != self.stream:
+                raise RuntimeError(
+                    "PreparedFFN must run on its preparation stream; concurrent reuse is unsupported")
+            self.artifact(*self.tensors, stream.cuda_stream)
+        p = self.plan.problem
+        return self.storage[4][:p.m, :p.n].view(p.output_shape)
+
+
+def prepare_ffn(x, weight1, weight2, *, up_impl="basic", down_impl="basic", block_num=None,
+                layout="linear", gelu="erf", up_variant=None, down_variant=None):
+    """Validate, plan, check the device, pad/contiguise and bind the kernels; no FFN launch.
+
+    Follows ops/api.py:48-89.  Padding and contiguisation are auxiliary device
+    operations timed outside the FFN.  up_variant/down_variant force a compiled
+    tile variant (tuning); None lets the library choose.
+    """
+    from .host.dispatch import compile_kernel
+    from . import _lib
+
+    p = validate_tensors(x, weight1, weight2, layout=layout, require_device=True)
+    selection = Selection(up_impl, down_impl)
+    selection.require_available()
+    import torch
+    verify_dependency()
+    device = x.device.index if x.device.index is not None else torch.cuda.current_device()
+    cu_count, _arch = _lib.query(device)
+    if block_num is None:
+        block_num = cu_count
+    plan = make_plan(p, selection, block_num, gelu=gelu, up_variant=up_variant,
+                     down_variant=down_variant)
+    if block_num > cu_count:
+        raise ValueError(f"block_num must not exceed the device CU count ({cu_count})")
+    with torch.cuda.device(x.device):
+        stream = torch.cuda.current_stream()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        storage = prepare_storage(x, weight1, weight2, plan)
+        end.record()
+        end.synchronize()
+        auxiliary_ms = start.elapsed_time(end)
+        tensors = tuple(t.data_ptr() for t in storage)
+        before = perf_counter()
+        try:
+            artifact, provenance = compile_kernel(plan)
+        except Exception as exc:
+            raise KernelCompilationError(f"{type(exc).__name__}: {exc}") from exc
+        preparation = {"auxiliary_device_interval_ms": auxiliary_ms,
+                       "compile_wall_ms": (perf_counter() - before) * 1000}
+    return PreparedFFN(plan, storage, tensors, artifact, provenance, preparation, stream)
+
+
+def ffn(x, weight1, weight2, **configuration):
+    """Y = GELU(X @ weight1.T) @ weight2.T; no bias, no autograd."""
+    return prepare_ffn(x, weight1, weight2, **configuration).run()

@@ -1,0 +1,49 @@
+// ffn_kernels.hip -- instantiates the GEMM engine for one (storage type, tile variant).
+//
+// Compiled once per pair with -DFFN_DT=<0 fp16|1 bf16> -DFFN_VARIANT=<id>; each object
+// exports one extern "C" launcher ffn_launch_d<DT>_v<VARIANT> used by ffn_mi355x.hip.
+#include "ffn_gemm.hpp"
+#include "ffn_variants.hpp"
+
+#if !defined(FFN_DT) || !defined(FFN_VARIANT)
+#error "compile with -DFFN_DT=<0|1> -DFFN_VARIANT=<id>"
+#endif
+
+namespace {
+template <int ID>
+struct VariantCfg;
+#define FFN_DEFINE_CFG(id, bm, bn, bk, wgm, wgn, st) \
+    template <>                                       \
+    struct VariantCfg<id> {                           \
+        using type = ffn::TileCfg<bm, bn, bk, wgm, wgn, st>; \
+    };
+FFN_VARIANTS(FFN_DEFINE_CFG)
+#undef FFN_DEFINE_CFG
+using Cfg = VariantCfg<FFN_VARIANT>::type;
+}  // namespace
+
+#define FFN_CAT_(a, b, c, d) a##b##c##d
+#define FFN_CAT(a, b, c, d) FFN_CAT_(a, b, c, d)
+#define FFN_LAUNCHER FFN_CAT(ffn_launch_d, FFN_DT, _v, FFN_VARIANT)
+
+extern "C" hipError_t FFN_LAUNCHER(int role, const ffn::GemmParams* p, int grid, hipStream_t stream) {
+    using namespace ffn;
+    const dim3 g(grid), b(Cfg::NT);
+    switch (role) {
+        case FFN_ROLE_UP_ERF:
+            hipLaunchKernelGGL((ffn_gemm_kernel<FFN_DT, Cfg, EPI_GELU_ERF, false>), g, b, 0, stream, *p);
+            break;
+        case FFN_ROLE_UP_RATIONAL:
+            hipLaunchKernelGGL((ffn_gemm_kernel<FFN_DT, Cfg, EPI_GELU_RATIONAL, false>), g, b, 0, stream, *p);
+            break;
+        case FFN_ROLE_DOWN_BASIC:
+            hipLaunchKernelGGL((ffn_gemm_kernel<FFN_DT, Cfg, EPI_STORE, false>), g, b, 0, stream, *p);
+            break;
+        case FFN_ROLE_DOWN_STREAMK:
+            hipLaunchKernelGGL((ffn_gemm_kernel<FFN_DT, Cfg, EPI_STORE, true>), g, b, 0, stream, *p);
+            break;
+        default:
+            return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}

@@ -1,0 +1,351 @@
+// ffn_mi355x.hip -- host side of libffn_mi355x.so: tile planning, Stream-K schedule,
+// launch sequencing and the extern "C" entry points declared in include/ffn_mi355x.h.
+//
+// The reference builds one artifact per FFN with tla.compile and launches it once
+// (ops/host/dispatch.py:97-116, ops/api.py:37-45); here the kernels are compiled ahead
+// of time for gfx950 and an FFN is two stream-ordered launches of the GEMM engine:
+// up-projection + GELU epilogue, then the Basic or Stream-K down-projection.  The
+// kernel boundary is the stage barrier that the reference builds from cross-core flags
+// (ops/kernel/ffn.py:371-376, 582-585).
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "ffn_gemm.hpp"
+#include "ffn_mi355x.h"
+#include "ffn_variants.hpp"
+
+#ifndef FFN_MI355X_REVISION
+#define FFN_MI355X_REVISION "unversioned"
+#endif
+
+typedef hipError_t (*ffn_launch_fn)(int role, const ffn::GemmParams* p, int grid, hipStream_t stream);
+
+#define FFN_DECLARE_LAUNCHERS(id, bm, bn, bk, wgm, wgn, st)                                      \
+    extern "C" hipError_t ffn_launch_d0_v##id(int, const ffn::GemmParams*, int, hipStream_t); \
+    extern "C" hipError_t ffn_launch_d1_v##id(int, const ffn::GemmParams*, int, hipStream_t);
+FFN_VARIANTS(FFN_DECLARE_LAUNCHERS)
+#undef FFN_DECLARE_LAUNCHERS
+
+namespace {
+
+struct Variant {
+    int bm, bn, bk, wgm, wgn, stages;
+    ffn_launch_fn launch[2];  // [dtype]
+    int waves() const { return wgm * wgn; }
+    int lds() const { return stages * (bm + bn) * bk * 2; }
+};
+
+#define FFN_VARIANT_ROW(id, bm, bn, bk, wgm, wgn, st) \
+    {bm, bn, bk, wgm, wgn, st, {ffn_launch_d0_v##id, ffn_launch_d1_v##id}},
+const Variant kVariants[] = {FFN_VARIANTS(FFN_VARIANT_ROW)};
+#undef FFN_VARIANT_ROW
+constexpr int kNumVariants = (int)(sizeof(kVariants) / sizeof(kVariants[0]));
+static_assert(kNumVariants == FFN_NUM_VARIANTS, "variant table");
+
+thread_local std::string g_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return code;
+}
+
+int ok() {
+    g_error.clear();
+    return FFN_MI355X_OK;
+}
+
+long long cdiv(long long a, long long b) { return (a + b - 1) / b; }
+
+// Relative MFMA efficiency of a macro tile.  A tile's work per byte staged through LDS and
+// L2 grows with BM*BN/(BM+BN); 256x256 is the reference point.
+double tile_eff(const Variant& v) {
+    const double intensity = (double)v.bm * v.bn / (double)(v.bm + v.bn);
+    return intensity >= 128.0 ? 1.0 : intensity / 128.0;
+}
+
+// Estimated time (arbitrary units) of a data-parallel GEMM over [M x N] with K depth.
+double cost_basic(const Variant& v, long long M, long long N, long long K, int G) {
+    const long long T = cdiv(M, v.bm) * cdiv(N, v.bn);
+    const long long waves = cdiv(T, G);
+    return (double)waves * v.bm * v.bn * (double)(cdiv(K, v.bk) * v.bk) / tile_eff(v);
+}
+
+struct SkShape {
+    long long tiles, k_iters, dp, sk, q, r, slots;
+};
+
+bool sk_shape(const Variant& v, long long M, long long N, long long K, int G, SkShape& s) {
+    s.tiles = cdiv(M, v.bm) * cdiv(N, v.bn);
+    s.k_iters = cdiv(K, v.bk);
+    s.sk = s.tiles % G;
+    s.dp = s.tiles - s.sk;
+    const long long total = s.sk * s.k_iters;
+    s.q = total / G;
+    s.r = total % G;
+    const long long span = s.q + (s.r ? 1 : 0);
+    // a range of `span` iterations touches at most ceil(span / k_iters) + 1 tiles
+    s.slots = cdiv(span, s.k_iters) + 1;
+    return s.sk > 0 && s.k_iters >= 2;
+}
+
+double cost_streamk(const Variant& v, const SkShape& s, int G) {
+    const double it = (double)v.bm * v.bn * v.bk / tile_eff(v);
+    const long long dp_waves = cdiv(s.dp, G);
+    const long long sk_iters = s.q + (s.r ? 1 : 0);
+    // publishing and re-reading an FP32 partial costs about two K-iterations of the tile
+    const double fixup = (s.k_iters > sk_iters) ? 2.0 : 0.0;
+    return it * ((double)dp_waves * s.k_iters + (double)sk_iters + fixup);
+}
+
+int pick_basic(long long M, long long N, long long K, int G) {
+    int best = 0;
+    double best_cost = 1e300;
+    for (int i = 0; i < kNumVariants; ++i) {
+        const double c = cost_basic(kVariants[i], M, N, K, G);
+        if (c < best_cost) best_cost = c, best = i;
+    }
+    return best;
+}
+
+int pick_streamk(long long M, long long N, long long K, int G) {
+    int best = -1;
+    double best_cost = 1e300;
+    for (int i = 0; i < kNumVariants; ++i) {
+        SkShape s;
+        if (!sk_shape(kVariants[i], M, N, K, G, s)) continue;
+        const double c = cost_streamk(kVariants[i], s, G);
+        if (c < best_cost) best_cost = c, best = i;
+    }
+    return best;
+}
+
+int group_m_for(long long tiles_m) { return (int)(tiles_m < 8 ? tiles_m : 8); }
+
+bool valid_plan(const ffn_mi355x_plan* p) {
+    return p && p->up_variant >= 0 && p->up_variant < kNumVariants && p->down_variant >= 0 &&
+           p->down_variant < kNumVariants && (p->dtype == 0 || p->dtype == 1) &&
+           (p->down_impl == FFN_MI355X_DOWN_BASIC || p->down_impl == FFN_MI355X_DOWN_STREAMK) &&
+           (p->gelu == 0 || p->gelu == 1) && p->block_num >= 1;
+}
+
+int launch(const Variant& v, int dtype, int role, const ffn::GemmParams& gp, int grid,
+           void* stream) {
+    const hipError_t e = v.launch[dtype](role, &gp, grid, (hipStream_t)stream);
+    if (e != hipSuccess)
+        return fail(FFN_MI355X_EHIP, "kernel launch failed: %s", hipGetErrorString(e));
+    return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int ffn_mi355x_query(int device, int* cu_count, char* arch, int arch_len) {
+    hipDeviceProp_t prop;
+    const hipError_t e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess)
+        return fail(FFN_MI355X_EHIP, "hipGetDeviceProperties(%d): %s", device, hipGetErrorString(e));
+    if (cu_count) *cu_count = prop.multiProcessorCount;
+    if (arch && arch_len > 0) {
+        strncpy(arch, prop.gcnArchName, (size_t)arch_len - 1);
+        arch[arch_len - 1] = '\0';
+    }
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(FFN_MI355X_EDEVICE, "This implementation targets gfx950 (MI355X) only, got %s",
+                    prop.gcnArchName);
+    return ok();
+}
+
+int ffn_mi355x_make_plan(int mp, int kp, int hp, int np, int dtype, int down_impl, int gelu,
+                         int block_num, int up_variant, int down_variant, ffn_mi355x_plan* plan) {
+    if (!plan) return fail(FFN_MI355X_EINVAL, "plan must not be NULL");
+    if (dtype != FFN_MI355X_FP16 && dtype != FFN_MI355X_BF16)
+        return fail(FFN_MI355X_EINVAL, "dtype must be float16 or bfloat16");
+    if (gelu != FFN_MI355X_GELU_ERF && gelu != FFN_MI355X_GELU_RATIONAL)
+        return fail(FFN_MI355X_EINVAL, "gelu must be erf or rational");
+    if (down_impl == FFN_MI355X_DOWN_FULL_LOAD_A || down_impl == FFN_MI355X_DOWN_FULL_LOAD_B)
+        return fail(FFN_MI355X_EUNAVAILABLE, "%s: no gfx950 kernel is provided for this down variant; no fallback",
+                    down_impl == FFN_MI355X_DOWN_FULL_LOAD_A ? "full_load_a" : "full_load_b");
+    if (down_impl != FFN_MI355X_DOWN_BASIC && down_impl != FFN_MI355X_DOWN_STREAMK)
+        return fail(FFN_MI355X_EINVAL, "Unknown down_impl: %d", down_impl);
+    if (block_num < 1 || block_num > 65535)
+        return fail(FFN_MI355X_EINVAL,
+                    "block_num must be a positive integer; hardware limit checked before launch");
+    if (mp <= 0 || kp <= 0 || hp <= 0 || np <= 0 || mp % 64 || hp % 64 || np % 64 || kp % 16)
+        return fail(FFN_MI355X_EINVAL,
+                    "padded extents must be positive, M/H/N multiples of 64 and K a multiple of 16 "
+                    "(got mp=%d kp=%d hp=%d np=%d)", mp, kp, hp, np);
+    if (kp > 65536 || hp > 65536 || np > 65536 || mp > INT_MAX - 256)
+        return fail(FFN_MI355X_EINVAL, "Shape exceeds the supported bounds");
+    if (up_variant >= kNumVariants || down_variant >= kNumVariants)
+        return fail(FFN_MI355X_EINVAL, "tile variant out of range (0..%d)", kNumVariants - 1);
+
+    memset(plan, 0, sizeof *plan);
+    plan->mp = mp, plan->kp = kp, plan->hp = hp, plan->np = np;
+    plan->dtype = dtype, plan->down_impl = down_impl, plan->gelu = gelu, plan->block_num = block_num;
+    const int G = block_num;
+
+    // up: [mp x hp], depth kp
+    const int uv = up_variant >= 0 ? up_variant : pick_basic(mp, hp, kp, G);
+    const Variant& U = kVariants[uv];
+    plan->up_variant = uv;
+    plan->up_bm = U.bm, plan->up_bn = U.bn, plan->up_bk = U.bk;
+    plan->up_tiles = (int)(cdiv(mp, U.bm) * cdiv(hp, U.bn));
+    plan->up_grid = plan->up_tiles < G ? plan->up_tiles : G;
+
+    // down: [mp x np], depth hp
+    int dv;
+    if (down_impl == FFN_MI355X_DOWN_STREAMK) {
+        if (down_variant >= 0) {
+            SkShape s;
+            if (!sk_shape(kVariants[down_variant], mp, np, hp, G, s)) {
+                if (s.k_iters < 2)
+                    return fail(FFN_MI355X_ENOT_APPLICABLE,
+                                "Stream-K candidate requires at least two K tiles along H");
+                return fail(FFN_MI355X_ENOT_APPLICABLE,
+                            "Stream-K candidate has no remainder tiles for this block_num");
+            }
+            dv = down_variant;
+        } else {
+            dv = pick_streamk(mp, np, hp, G);
+            if (dv < 0) {
+                bool any_two = false;
+                for (int i = 0; i < kNumVariants; ++i) any_two |= cdiv(hp, kVariants[i].bk) >= 2;
+                if (!any_two)
+                    return fail(FFN_MI355X_ENOT_APPLICABLE,
+                                "Stream-K candidate requires at least two K tiles along H");
+                return fail(FFN_MI355X_ENOT_APPLICABLE,
+                            "Stream-K candidate has no remainder tiles for this block_num");
+            }
+        }
+    } else {
+        dv = down_variant >= 0 ? down_variant : pick_basic(mp, np, hp, G);
+    }
+    const Variant& D = kVariants[dv];
+    plan->down_variant = dv;
+    plan->down_bm = D.bm, plan->down_bn = D.bn, plan->down_bk = D.bk;
+    plan->down_tiles = (int)(cdiv(mp, D.bm) * cdiv(np, D.bn));
+    plan->down_k_iters = (int)cdiv(hp, D.bk);
+    if (down_impl == FFN_MI355X_DOWN_STREAMK) {
+        SkShape s;
+        sk_shape(D, mp, np, hp, G, s);
+        plan->down_dp_tiles = (int)s.dp;
+        plan->down_sk_tiles = (int)s.sk;
+        plan->down_slots_per_wg = (int)s.slots;
+        plan->down_grid = G;
+        const size_t partials = (size_t)G * (size_t)s.slots * (size_t)D.bm * (size_t)D.bn * 4u;
+        const size_t counters = ((size_t)s.sk * 4u + 255u) / 256u * 256u;
+        plan->workspace_bytes = partials + counters;
+    } else {
+        plan->down_dp_tiles = plan->down_tiles;
+        plan->down_grid = plan->down_tiles < G ? plan->down_tiles : G;
+        plan->workspace_bytes = 0;
+    }
+    return ok();
+}
+
+int ffn_mi355x_workspace_bytes(const ffn_mi355x_plan* plan, size_t* bytes) {
+    if (!plan || !bytes) return fail(FFN_MI355X_EINVAL, "NULL argument");
+    *bytes = plan->workspace_bytes;
+    return ok();
+}
+
+int ffn_mi355x_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, void* hidden,
+                  void* hip_stream) {
+    if (!valid_plan(plan)) return fail(FFN_MI355X_EINVAL, "invalid plan");
+    if (!x || !w1 || !hidden) return fail(FFN_MI355X_EINVAL, "NULL device buffer");
+    const Variant& U = kVariants[plan->up_variant];
+    ffn::GemmParams gp;
+    memset(&gp, 0, sizeof gp);
+    gp.a = x, gp.b = w1, gp.c = hidden;
+    gp.M = plan->mp, gp.N = plan->hp, gp.K = plan->kp;
+    gp.lda = plan->kp, gp.ldb = plan->kp, gp.ldc = plan->hp;
+    gp.tiles_m = (int)cdiv(plan->mp, U.bm), gp.tiles_n = (int)cdiv(plan->hp, U.bn);
+    gp.k_iters = (int)cdiv(plan->kp, U.bk);
+    gp.dp_tiles = gp.tiles_m * gp.tiles_n;
+    gp.group_m = group_m_for(gp.tiles_m);
+    const int role = plan->gelu == FFN_MI355X_GELU_ERF ? FFN_ROLE_UP_ERF : FFN_ROLE_UP_RATIONAL;
+    return launch(U, plan->dtype, role, gp, plan->up_grid, hip_stream);
+}
+
+int ffn_mi355x_down(const ffn_mi355x_plan* plan, const void* hidden, const void* w2, void* out,
+                    void* ws, void* hip_stream) {
+    if (!valid_plan(plan)) return fail(FFN_MI355X_EINVAL, "invalid plan");
+    if (!hidden || !w2 || !out) return fail(FFN_MI355X_EINVAL, "NULL device buffer");
+    const Variant& D = kVariants[plan->down_variant];
+    ffn::GemmParams gp;
+    memset(&gp, 0, sizeof gp);
+    gp.a = hidden, gp.b = w2, gp.c = out;
+    gp.M = plan->mp, gp.N = plan->np, gp.K = plan->hp;
+    gp.lda = plan->hp, gp.ldb = plan->hp, gp.ldc = plan->np;
+    gp.tiles_m = (int)cdiv(plan->mp, D.bm), gp.tiles_n = (int)cdiv(plan->np, D.bn);
+    gp.k_iters = plan->down_k_iters;
+    gp.group_m = group_m_for(gp.tiles_m);
+    if (plan->down_impl == FFN_MI355X_DOWN_STREAMK) {
+        if (!ws) return fail(FFN_MI355X_EINVAL, "Stream-K needs a workspace of %zu bytes", plan->workspace_bytes);
+        const int G = plan->down_grid;
+        gp.dp_tiles = plan->down_dp_tiles;
+        gp.sk_tiles = plan->down_sk_tiles;
+        const long long total = (long long)plan->down_sk_tiles * plan->down_k_iters;
+        gp.sk_q = (int)(total / G);
+        gp.sk_r = (int)(total % G);
+        gp.slots_per_wg = plan->down_slots_per_wg;
+        gp.ws = (float*)ws;
+        gp.counters = (unsigned*)((char*)ws + (size_t)G * plan->down_slots_per_wg * D.bm * D.bn * 4u);
+        return launch(D, plan->dtype, FFN_ROLE_DOWN_STREAMK, gp, G, hip_stream);
+    }
+    gp.dp_tiles = plan->down_tiles;
+    return launch(D, plan->dtype, FFN_ROLE_DOWN_BASIC, gp, plan->down_grid, hip_stream);
+}
+
+int ffn_mi355x_run(const ffn_mi355x_plan* plan, const void* x, const void* w1, const void* w2,
+                   void* hidden, void* out, void* ws, void* hip_stream) {
+    int rc = ffn_mi355x_up(plan, x, w1, hidden, hip_stream);
+    if (rc != FFN_MI355X_OK) return rc;
+    return ffn_mi355x_down(plan, hidden, w2, out, ws, hip_stream);
+}
+
+int ffn_mi355x_num_variants(void) { return kNumVariants; }
+
+int ffn_mi355x_variant_info(int variant, int* bm, int* bn, int* bk, int* waves, int* stages,
+                            int* lds_bytes) {
+    if (variant < 0 || variant >= kNumVariants)
+        return fail(FFN_MI355X_EINVAL, "tile variant out of range (0..%d)", kNumVariants - 1);
+    const Variant& v = kVariants[variant];
+    if (bm) *bm = v.bm;
+    if (bn) *bn = v.bn;
+    if (bk) *bk = v.bk;
+    if (waves) *waves = v.waves();
+    if (stages) *stages = v.stages;
+    if (lds_bytes) *lds_bytes = v.lds();
+    return ok();
+}
+
+const char* ffn_mi355x_last_error(void) { return g_error.c_str(); }
+
+const char* ffn_mi355x_strerror(int code) {
+    switch (code) {
+        case FFN_MI355X_OK: return "ok";
+        case FFN_MI355X_EINVAL: return "invalid argument";
+        case FFN_MI355X_ENOT_APPLICABLE: return "not applicable";
+        case FFN_MI355X_EUNAVAILABLE: return "unavailable";
+        case FFN_MI355X_EHIP: return "HIP runtime error";
+        case FFN_MI355X_EDEVICE: return "unsupported device";
+        default: return "unknown error";
+    }
+}
+
+const char* ffn_mi355x_version(void) { return "ffn_mi355x gfx950 " FFN_MI355X_REVISION; }
+
+}  // extern "C"

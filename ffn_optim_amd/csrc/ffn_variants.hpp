@@ -1,0 +1,19 @@
+// ffn_variants.hpp -- the macro-tile variants compiled into libffn_mi355x.so.
+//
+// X(id, BM, BN, BK, waves along M, waves along N, LDS stages)
+// Each variant is built for both storage types and four epilogues (GELU-erf,
+// GELU-rational, plain store, plain store + Stream-K split) in its own object.
+#pragma once
+
+#define FFN_VARIANTS(X)                 \
+    X(0, 256, 256, 64, 2, 2, 2)         \
+    X(1, 256, 128, 64, 2, 2, 3)         \
+    X(2, 128, 256, 64, 2, 2, 3)         \
+    X(3, 128, 128, 64, 2, 2, 2)         \
+    X(4, 64, 64, 64, 2, 2, 2)           \
+    X(5, 64, 128, 64, 2, 2, 3)
+
+#define FFN_NUM_VARIANTS 6
+
+// launch roles of one variant
+enum { FFN_ROLE_UP_ERF = 0, FFN_ROLE_UP_RATIONAL = 1, FFN_ROLE_DOWN_BASIC = 2, FFN_ROLE_DOWN_STREAMK = 3 };

@@ -1,0 +1,113 @@
+"""Padding, tile choice and Stream-K applicability (restates ops/host/tiling.py).
+
+Padding units are the reference's (M/H/N to 64, K to 16, tiling.py:63-64).  The
+tile geometry and the Stream-K schedule are decided by the native library
+(``ffn_mi355x_make_plan``) so that the C ABI plans exactly as this host does;
+this module mirrors its result into the reference's Plan/Tile shape.
+"""
+from __future__ import annotations
+
+from dataclasses import asdict, dataclass
+
+from .dispatch import Selection
+from .inputs import Problem
+
+MI355X_CU_COUNT = 256
+DEFAULT_BLOCK_NUM = MI355X_CU_COUNT
+
+
+def align(value, unit):
+    return (value + unit - 1) // unit * unit
+
+
+@dataclass(frozen=True)
+class Tile:
+    """Macro tile of one GEMM (elements): bm x bn output, bk deep per LDS stage.
+
+    waves is the number of 64-lane wavefronts per workgroup, stages the number of
+    LDS buffers, variant the id of the compiled kernel variant.
+    """
+
+    bm: int
+    bn: int
+    bk: int
+    waves: int
+    stages: int
+    variant: int
+
+
+@dataclass(frozen=True)
+class Plan:
+    """Everything one FFN launch sequence needs (reference Plan, tiling.py:28-55).
+
+    block_num is the persistent-workgroup count of both launches; mp/kp/hp/np are
+    the padded extents; workspace_shape is the FP32 Stream-K scratch ((1, 1) and
+    unused for the Basic down).  native is the C plan handed to the library.
+    """
+
+    problem: Problem
+    selection: Selection
+    block_num: int
+    mp: int
+    kp: int
+    hp: int
+    np: int
+    up: Tile
+    down: Tile
+    workspace_shape: tuple[int, int]
+    gelu: str = "erf"
+    native: object = None
+
+    @property
+    def workspace_bytes(self):
+        return self.workspace_shape[0] * self.workspace_shape[1] * 4
+
+    def schedule(self):
+        """Launch shape and Stream-K split of the down GEMM (from the native plan)."""
+        n = self.native
+        return {"up_tiles": n.up_tiles, "up_grid": n.up_grid, "down_tiles": n.down_tiles,
+                "down_grid": n.down_grid, "down_k_iters": n.down_k_iters,
+                "down_dp_tiles": n.down_dp_tiles, "down_sk_tiles": n.down_sk_tiles,
+                "down_slots_per_wg": n.down_slots_per_wg}
+
+    def to_dict(self):
+        d = {k: v for k, v in asdict(self).items() if k != "native"}
+        d["schedule"] = self.schedule() if self.native is not None else None
+        return d
+
+
+def _tile(bm, bn, bk, variant):
+    from .. import _lib
+    info = _lib.variants()[variant]
+    return Tile(bm, bn, bk, info["waves"], info["stages"], variant)
+
+
+def make_plan(problem, selection=Selection(), block_num=DEFAULT_BLOCK_NUM, *, gelu="erf",
+              up_variant=None, down_variant=None):
+    """Plan one FFN (ops/host/tiling.py:58-74).
+
+    Raises DependencyUnavailable for full_load_*, ValueError for a block_num outside
+    [1, 65535], NotApplicable when Stream-K has no remainder tiles for this
+    block_num or H spans fewer than two K iterations.
+    """
+    from .. import _lib
+    from .dispatch import GELU_FORMS
+
+    selection.require_available()
+    if type(block_num) is not int or not 1 <= block_num <= 65535:
+        raise ValueError("block_num must be a positive integer; hardware limit checked before launch")
+    if gelu not in GELU_FORMS:
+        raise ValueError(f"gelu must be one of {GELU_FORMS}")
+    mp, kp = align(problem.m, 64), align(problem.k, 16)
+    hp, np_ = align(problem.h, 64), align(problem.n, 64)
+    dtype = _lib.BF16 if problem.dtype == "bfloat16" else _lib.FP16
+    native = _lib.make_plan(mp, kp, hp, np_, dtype, selection.down_impl, gelu, block_num,
+                            -1 if up_variant is None else up_variant,
+                            -1 if down_variant is None else down_variant)
+    up = _tile(native.up_bm, native.up_bn, native.up_bk, native.up_variant)
+    down = _tile(native.down_bm, native.down_bn, native.down_bk, native.down_variant)
+    if selection.down_impl == "streamk":
+        workspace = (native.workspace_bytes // 256, 64)
+    else:
+        workspace = (1, 1)  # unused argument, never read by the Basic down
+    return Plan(problem, selection, block_num, mp, kp, hp, np_, up, down, workspace, gelu, native)

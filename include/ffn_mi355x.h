@@ -1,0 +1,122 @@
+/*
+ * ffn_mi355x.h -- C ABI of the MI355X (gfx950) fused FFN operator
+ *
+ *     Y = GELU(X . W1^T) . W2^T        X [mp,kp], W1 [hp,kp], W2 [np,hp]
+ *
+ * Every buffer is a device pointer to a row-major, K-contiguous matrix that the
+ * caller has already contiguised and zero-padded (M/H/N to 64, K to 16), exactly
+ * as ops/host/inputs.py:74-90 stores them in the reference.  The library never
+ * allocates or frees device memory, never synchronises the host, and enqueues
+ * all work on the HIP stream it is given, so it is stream-ordered like the
+ * single artifact launch it replaces (ops/api.py:37-45).
+ *
+ * Return codes are 0 on success or one of the negative FFN_MI355X_E* values;
+ * ffn_mi355x_last_error() gives the message of the last failure on the calling
+ * thread.  The Python host maps them onto the reference's exception taxonomy
+ * (ops/api.py:9-14, ops/host/dispatch.py:22-39).
+ */
+#ifndef FFN_MI355X_H
+#define FFN_MI355X_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element type of X, W1, W2, hidden and the output */
+#define FFN_MI355X_FP16 0
+#define FFN_MI355X_BF16 1
+
+/* down-projection implementation (ops/host/dispatch.py:15 DOWN_IMPLS) */
+#define FFN_MI355X_DOWN_BASIC 0
+#define FFN_MI355X_DOWN_STREAMK 1
+#define FFN_MI355X_DOWN_FULL_LOAD_A 2 /* reported unavailable, no fallback */
+#define FFN_MI355X_DOWN_FULL_LOAD_B 3 /* reported unavailable, no fallback */
+
+/* GELU form applied in the up-projection epilogue */
+#define FFN_MI355X_GELU_ERF 0      /* 0.5*z*(1+erf(z/sqrt2)), F.gelu(approximate='none') */
+#define FFN_MI355X_GELU_RATIONAL 1 /* clamp + P5/Q5 rational erf, validation/reference.py:5-13 */
+
+/* return codes */
+#define FFN_MI355X_OK 0
+#define FFN_MI355X_EINVAL (-1)          /* ValueError */
+#define FFN_MI355X_ENOT_APPLICABLE (-2) /* NotApplicable(ValueError) */
+#define FFN_MI355X_EUNAVAILABLE (-3)    /* DependencyUnavailable(RuntimeError) */
+#define FFN_MI355X_EHIP (-4)            /* RuntimeError from the HIP runtime */
+#define FFN_MI355X_EDEVICE (-5)         /* RuntimeError: not a gfx950 device */
+
+/* Tile geometry and launch shape the library chose for one FFN.  It is the
+ * counterpart of the reference's Plan/Tile (ops/host/tiling.py:11-74). */
+typedef struct ffn_mi355x_plan {
+    int mp, kp, hp, np;          /* padded extents the plan was made for */
+    int dtype, down_impl, gelu;
+    int block_num;               /* persistent workgroups per launch (<= CU count) */
+    int up_variant, down_variant;
+    int up_bm, up_bn, up_bk;     /* up-projection macro tile (M x H x K) */
+    int down_bm, down_bn, down_bk; /* down-projection macro tile (M x N x H) */
+    int up_tiles, up_grid;
+    int down_tiles, down_grid;
+    int down_k_iters;            /* BK-deep iterations along H per down tile */
+    int down_dp_tiles;           /* tiles reduced whole by one workgroup */
+    int down_sk_tiles;           /* tiles whose H-range is split over workgroups */
+    int down_slots_per_wg;       /* FP32 partial-tile slots per workgroup */
+    size_t workspace_bytes;      /* FP32 partials + per-tile arrival counters */
+} ffn_mi355x_plan;
+
+/* Device check replacing the Ascend950/AIC checks of ops/api.py:58-66:
+ * writes the CU count and gcnArchName of `device`; FFN_MI355X_EDEVICE if the
+ * device is not gfx950. */
+int ffn_mi355x_query(int device, int* cu_count, char* arch, int arch_len);
+
+/* Tile selection and Stream-K schedule, host-only (no device call).  Mirrors
+ * make_plan (ops/host/tiling.py:58-74): FFN_MI355X_EUNAVAILABLE for the
+ * full-load down variants (ops/host/dispatch.py:61-66), FFN_MI355X_EINVAL for a
+ * block_num outside [1, 65535], FFN_MI355X_ENOT_APPLICABLE for Stream-K shapes
+ * with no remainder tiles or fewer than two H iterations (tiling.py:65-70).
+ * up_variant / down_variant < 0 let the library choose; >= 0 forces a tile. */
+int ffn_mi355x_make_plan(int mp, int kp, int hp, int np, int dtype, int down_impl,
+                         int gelu, int block_num, int up_variant, int down_variant,
+                         ffn_mi355x_plan* plan);
+
+/* Workspace bytes a plan needs (0 for the Basic down). */
+int ffn_mi355x_workspace_bytes(const ffn_mi355x_plan* plan, size_t* bytes);
+
+/* The whole FFN: up GEMM + GELU epilogue writing `hidden` [mp,hp] in the input
+ * dtype, then the Basic or Stream-K down GEMM writing `out` [mp,np].  Replaces
+ * the single artifact(*tensors, block_num) launch of ops/api.py:43 built by
+ * compile_kernel (ops/host/dispatch.py:97-116) from ops/kernel/ffn.py.
+ * `ws` must hold plan->workspace_bytes and be zeroed once before first use;
+ * the Stream-K kernel leaves its arrival counters at zero again on exit. */
+int ffn_mi355x_run(const ffn_mi355x_plan* plan, const void* x, const void* w1,
+                   const void* w2, void* hidden, void* out, void* ws, void* hip_stream);
+
+/* Stage 1 alone: up-projection with GELU epilogue (ops/kernel/ffn.py:207-360,
+ * 540-581, the cube/vector up regions of both kernels). */
+int ffn_mi355x_up(const ffn_mi355x_plan* plan, const void* x, const void* w1,
+                  void* hidden, void* hip_stream);
+
+/* Stage 2 alone: Basic (ops/kernel/ffn.py:377-529) or Stream-K
+ * (ops/kernel/ffn.py:951-1423) down-projection. */
+int ffn_mi355x_down(const ffn_mi355x_plan* plan, const void* hidden, const void* w2,
+                    void* out, void* ws, void* hip_stream);
+
+/* Number of tile variants compiled in, and the geometry of one of them. */
+int ffn_mi355x_num_variants(void);
+int ffn_mi355x_variant_info(int variant, int* bm, int* bn, int* bk, int* waves, int* stages,
+                            int* lds_bytes);
+
+/* Message of the last failure on this thread ("" if none). */
+const char* ffn_mi355x_last_error(void);
+
+/* Text of a return code. */
+const char* ffn_mi355x_strerror(int code);
+
+/* Library build tag (target architecture and source revision). */
+const char* ffn_mi355x_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FFN_MI355X_H */

@@ -1,0 +1,122 @@
+"""Oracle -- TEST INFRASTRUCTURE ONLY, never part of the product path.
+
+CPU restatement of the reference's golden FFN, its error metric and its seeded
+input generator:
+
+  gelu_rational  validation/reference.py:5-13   rational erf GELU (FP32)
+  gelu_erf       validation/reference.py:19     F.gelu(approximate='none')
+  ffn_torch      validation/reference.py:16-23  FP32 matmul -> GELU -> [stage] -> matmul -> cast
+  compare        validation/test_ffn.py:6-21    mean(|o-g|/(|g|+1e-3)) < 0.05 (+ max_abs, rms)
+  make_inputs    common/cases.py:34-50          seeded randn x, w1*K^-1/2, w2*H^-1/2 (+ stride-2 view)
+
+Pinning (tests/test_oracle.py): the reference's own KATs (rational-vs-erf bound
+< 2e-5 on linspace(-10,10,10001); compare's bad-result cases), closed forms
+(math.erf), brute-force integer FFNs in pure Python, the independent C
+restatement oracle/ffn_ref.c (double accumulation), invariants (padding,
+odd symmetry, the clamp).  Nothing here is imported by ffn_optim_amd/.
+"""
+from __future__ import annotations
+
+from math import prod
+
+SQRT1_2 = 0.70710678118654752
+
+
+def gelu_rational(z):
+    """Rational erf GELU of the reference kernel, FP32 (validation/reference.py:5-13)."""
+    t = (z.float() * SQRT1_2).clamp(-3.92, 3.92)
+    t2 = t * t
+    p = (((((t2 * 0.053443748819 + 7.5517016694) * t2 + 101.62808918)
+            * t2 + 1393.8061484) * t2 + 5063.7915060) * t2 + 29639.384698) * t
+    q = ((((t2 + 31.212858877) * t2 + 398.56963806) * t2 + 3023.1248150)
+         * t2 + 13243.365831) * t2 + 26267.224157
+    return 0.5 * z.float() * (1 + p / q)
+
+
+def gelu_erf(z):
+    """Exact GELU 0.5*z*(1+erf(z/sqrt2)) in FP32 (validation/reference.py:19)."""
+    import torch.nn.functional as F
+    return F.gelu(z.float(), approximate="none")
+
+
+def shapes(x_shape, w1_shape, w2_shape):
+    """(m, k, h, n, output_shape) of an FFN, without the product's validation."""
+    h, k = w1_shape
+    n, h2 = w2_shape
+    assert x_shape[-1] == k and h == h2, "x[...,K], w1[H,K], w2[N,H]"
+    return prod(x_shape[:-1]), k, h, n, (*x_shape[:-1], n)
+
+
+def ffn_torch(x, weight1, weight2, *, staged=False, rational=False):
+    """Torch FP32 golden (validation/reference.py:16-23).
+
+    z = X[m,k].float() @ W1.float().T; hidden = GELU(z) (erf, or the rational
+    form); staged rounds hidden to the input dtype before the second matmul;
+    the result is cast once to the input dtype and reshaped to [..., N].
+    """
+    m, k, _, _, out_shape = shapes(tuple(x.shape), tuple(weight1.shape), tuple(weight2.shape))
+    z = x.reshape(m, k).float() @ weight1.float().T
+    hidden = gelu_rational(z) if rational else gelu_erf(z)
+    if staged:
+        hidden = hidden.to(x.dtype).float()
+    return (hidden @ weight2.float().T).to(x.dtype).reshape(out_shape)
+
+
+def ffn_rows(x, weight1, weight2, rows, **kw):
+    """ffn_torch on a subset of the rows of X (each output row depends on its X row only)."""
+    m, k, _, n, _ = shapes(tuple(x.shape), tuple(weight1.shape), tuple(weight2.shape))
+    xs = x.reshape(m, k)[rows]
+    return ffn_torch(xs, weight1, weight2, **kw)
+
+
+def compare(output, golden):
+    """Pass criterion of validation/test_ffn.py:6-21 (shape, dtype, finiteness, mean_rel < 0.05)."""
+    import torch
+    result = {"passed": False, "shape_ok": tuple(output.shape) == tuple(golden.shape),
+              "dtype_ok": output.dtype == golden.dtype, "finite": False,
+              "max_abs": None, "rms": None, "mean_rel": None}
+    if not result["shape_ok"] or not result["dtype_ok"]:
+        return result
+    a, b = output.detach().float(), golden.detach().float()
+    result["finite"] = bool(torch.isfinite(a).all() and torch.isfinite(b).all())
+    if not result["finite"] or not a.numel():
+        return result
+    d = (a - b).abs()
+    result.update(max_abs=d.max().item(), rms=d.square().mean().sqrt().item(),
+                  mean_rel=(d / (b.abs() + 1e-3)).mean().item())
+    result["passed"] = result["mean_rel"] < 0.05
+    return result
+
+
+def make_inputs(case, device="cpu"):
+    """Deterministic inputs of one case (common/cases.py:34-50).
+
+    One CPU generator seeded with case['seed']; randn FP32 sampled in the order
+    x (scale 1), w1 (K^-1/2), w2 (H^-1/2), cast to the dtype, moved to `device`.
+    noncontiguous=True returns stride-2 views of twice-as-wide buffers.
+    """
+    import torch
+    x_shape = tuple(case["shape"])
+    h, k = case["weight1_shape"]
+    n, _ = case["weight2_shape"]
+    generator = torch.Generator(device="cpu").manual_seed(case.get("seed", 0))
+    dtype = getattr(torch, case["dtype"])
+
+    def sample(shape, scale=1.0):
+        return (torch.randn(shape, generator=generator) * scale).to(dtype).to(device)
+
+    x = sample(x_shape)
+    w1 = sample((h, k), k ** -0.5)
+    w2 = sample((n, h), h ** -0.5)
+    if case.get("noncontiguous", False):
+        def strided(t):
+            buf = torch.empty((*t.shape[:-1], t.shape[-1] * 2), dtype=t.dtype, device=t.device)
+            buf[..., ::2].copy_(t)
+            return buf[..., ::2]
+        x, w1, w2 = map(strided, (x, w1, w2))
+    return x, w1, w2
+
+
+def transposed_view(x):
+    """Same values, strides of a dim-1/dim-2 transposed buffer (the unaligned 4-D case)."""
+    return x.transpose(1, 2).contiguous().transpose(1, 2)

@@ -1,0 +1,234 @@
+"""GPU parity of the HIP FFN against the oracle (the reference's torch FP32 golden).
+
+Every test runs the gfx950 kernels through libffn_mi355x.so and checks them with
+the reference criterion compare() (mean_rel < 0.05, max_abs and rms reported),
+or bit-exactly where the arithmetic is exact (integer-valued operands).
+"""
+import ctypes
+
+import pytest
+import torch
+
+from ffn_optim_amd import _lib, prepare_ffn
+from ffn_optim_amd.cases import V1_CASES, get_case, load_cases, make_inputs
+from oracle.reference import compare, ffn_rows, ffn_torch, gelu_erf, gelu_rational
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = {"float16": torch.float16, "bfloat16": torch.bfloat16}
+
+
+def say(*args):
+    print("[gpu-test]", *args, flush=True)
+
+
+def run_prepared(x, w1, w2, **kw):
+    prepared = prepare_ffn(x, w1, w2, **kw)
+    out = prepared.run()
+    torch.cuda.synchronize()
+    return prepared, out
+
+
+@pytest.mark.parametrize("down", ["basic", "streamk"])
+@pytest.mark.parametrize("case_id", ["c1_smoke_fp16", "c2_aligned_bf16", "c3_unaligned_fp16",
+                                     "c4_decode_bf16"])
+def test_baseline_case_full(case_id, down):
+    case = get_case(case_id)
+    say(case_id, down)
+    x, w1, w2 = make_inputs(case, "cuda")
+    prepared, out = run_prepared(x, w1, w2, down_impl=down)
+    golden = ffn_torch(x.cpu(), w1.cpu(), w2.cpu())
+    res = compare(out.cpu(), golden)
+    say(case_id, down, prepared.plan.up, prepared.plan.down, res)
+    assert res["passed"], res
+    assert out.shape == golden.shape
+
+
+@pytest.mark.parametrize("down", ["basic", "streamk"])
+def test_dit_case_sampled_rows(down):
+    """Large-M case: every output row depends only on its X row, so a seeded row sample
+    of the golden checks the full-size launch."""
+    case = get_case("c5_dit_bf16")
+    say("c5", down)
+    x, w1, w2 = make_inputs(case, "cuda")
+    prepared, out = run_prepared(x, w1, w2, down_impl=down)
+    m = x.numel() // x.shape[-1]
+    rows = torch.randperm(m, generator=torch.Generator().manual_seed(7))[:384]
+    golden = ffn_rows(x.cpu(), w1.cpu(), w2.cpu(), rows)
+    got = out.reshape(m, -1)[rows.cuda()].cpu()
+    res = compare(got, golden)
+    say("c5", down, res)
+    assert res["passed"], res
+
+
+@pytest.mark.parametrize("down", ["basic", "streamk"])
+@pytest.mark.parametrize("case", load_cases(V1_CASES), ids=lambda c: c["case_id"])
+def test_reference_smoke_cases(case, down):
+    say(case["case_id"], down)
+    x, w1, w2 = make_inputs(case, "cuda")
+    try:
+        prepared, out = run_prepared(x, w1, w2, down_impl=down)
+    except ValueError as exc:  # NotApplicable is a ValueError
+        assert down == "streamk", exc
+        pytest.skip(f"streamk not applicable: {exc}")
+    golden = ffn_torch(x.cpu(), w1.cpu(), w2.cpu())
+    staged = ffn_torch(x.cpu(), w1.cpu(), w2.cpu(), staged=True)
+    res, res_staged = compare(out.cpu(), golden), compare(out.cpu(), staged)
+    say(case["case_id"], down, res, res_staged)
+    assert res["passed"] and res_staged["passed"]
+    assert out.shape == tuple(case["shape"][:-1]) + (case["weight2_shape"][0],)
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("rank", [2, 3, 5, 8])
+def test_ranks_noncontiguous_padding(rank, dtype):
+    """Restates validation/test_ffn.py:31-48 on the device: stride-2 inputs, ranks 2-8."""
+    dt = DTYPES[dtype]
+    g = torch.Generator().manual_seed(rank)
+    shape = (1,) * (rank - 2) + (3, 17)
+    x = torch.randn((*shape[:-1], 34), generator=g).to(dt)[..., ::2]
+    w1 = torch.randn(19, 34, generator=g).to(dt)[:, ::2]
+    w2 = torch.randn(23, 38, generator=g).to(dt)[:, ::2]
+    _, out = run_prepared(x.cuda(), w1.cuda(), w2.cuda())
+    ref = ffn_torch(x, w1, w2, staged=True)
+    res = compare(out.cpu(), ref)
+    assert res["passed"], res
+    assert out.shape == (*shape[:-1], 23)
+
+
+@pytest.mark.parametrize("down", ["basic", "streamk"])
+def test_rational_gelu_option(down):
+    case = get_case("c2_aligned_bf16")
+    x, w1, w2 = make_inputs(case, "cuda")
+    _, out = run_prepared(x, w1, w2, down_impl=down, gelu="rational")
+    golden = ffn_torch(x.cpu(), w1.cpu(), w2.cpu(), staged=True, rational=True)
+    res = compare(out.cpu(), golden)
+    say("rational", down, res)
+    assert res["passed"], res
+
+
+def test_repeat_calls_bitwise_and_poisoned_buffers():
+    """First run + repeated runs must agree bit for bit (performance/run.py:198-219), also
+    when hidden/out start as NaN."""
+    case = get_case("c3_unaligned_fp16")
+    x, w1, w2 = make_inputs(case, "cuda")
+    for down in ("basic", "streamk"):
+        prepared = prepare_ffn(x, w1, w2, down_impl=down)
+        prepared.storage[3].fill_(float("nan"))
+        prepared.storage[4].fill_(float("nan"))
+        first = prepared.run().clone()
+        for _ in range(3):
+            again = prepared.run()
+            torch.cuda.synchronize()
+            assert torch.equal(first.view(torch.int16), again.view(torch.int16)), down
+        assert torch.isfinite(first).all()
+
+
+def test_wrong_stream_raises():
+    case = get_case("c1_smoke_fp16")
+    x, w1, w2 = make_inputs(case, "cuda")
+    prepared = prepare_ffn(x, w1, w2)
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        with pytest.raises(RuntimeError, match="preparation stream"):
+            prepared.run()
+    torch.cuda.synchronize()
+
+
+def test_block_num_above_cu_count_rejected():
+    case = get_case("c1_smoke_fp16")
+    x, w1, w2 = make_inputs(case, "cuda")
+    cus, arch = _lib.query(torch.cuda.current_device())
+    assert arch.startswith("gfx950")
+    with pytest.raises(ValueError):
+        prepare_ffn(x, w1, w2, block_num=cus + 1)
+
+
+# ---------------------------------------------------------------------------
+# bit-exact GEMM checks through the C ABI (integer-valued operands: every FP32
+# partial sum is an exact integer, so Basic, Stream-K and the golden must agree
+# to the last bit after the single RNE cast)
+# ---------------------------------------------------------------------------
+
+def _plan(mp, kp, hp, np_, dtype, down, block_num, upv=-1, downv=-1):
+    return _lib.make_plan(mp, kp, hp, np_, _lib.BF16 if dtype == torch.bfloat16 else _lib.FP16,
+                          down, "erf", block_num, upv, downv)
+
+
+def _int_tensor(shape, gen, lo=-2, hi=2):
+    return torch.randint(lo, hi + 1, shape, generator=gen).float()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_down_integer_bit_exact_all_variants(dtype):
+    lib = _lib.load()
+    gen = torch.Generator().manual_seed(11)
+    mp, hp, np_ = 320, 1024, 448      # ragged against every tile shape
+    hid = _int_tensor((mp, hp), gen).to(dtype)
+    w2 = _int_tensor((np_, hp), gen).to(dtype)
+    golden = (hid.double() @ w2.double().T).float().to(dtype)
+    hid_d, w2_d = hid.cuda(), w2.cuda()
+    stream = torch.cuda.current_stream().cuda_stream
+    nvar = lib.ffn_mi355x_num_variants()
+    for variant in range(nvar):
+        for down, block_num in (("basic", 256), ("basic", 7), ("streamk", 256), ("streamk", 37)):
+            try:
+                plan = _plan(mp, 64, hp, np_, dtype, down, block_num, 0, variant)
+            except ValueError:
+                continue
+            say("down-exact", dtype, variant, down, block_num, plan.to_dict())
+            out = torch.full((mp, np_), float("nan"), dtype=dtype, device="cuda")
+            ws = torch.zeros(max(1, plan.workspace_bytes // 4), dtype=torch.float32, device="cuda")
+            _lib.check(lib.ffn_mi355x_down(ctypes.byref(plan), hid_d.data_ptr(), w2_d.data_ptr(),
+                                           out.data_ptr(), ws.data_ptr(), stream))
+            torch.cuda.synchronize()
+            assert torch.equal(out.cpu().view(torch.int16), golden.view(torch.int16)), \
+                (variant, down, block_num)
+            if down == "streamk":  # arrival counters are re-armed to zero on exit
+                partial_bytes = (plan.down_grid * plan.down_slots_per_wg * plan.down_bm
+                                 * plan.down_bn * 4)
+                counters = ws.view(torch.int32)[partial_bytes // 4:
+                                                partial_bytes // 4 + plan.down_sk_tiles]
+                assert int(counters.abs().sum()) == 0
+
+
+def _ordinal(bits16):
+    """Bit patterns of a 16-bit float as points on a monotonic integer line (+0 == -0)."""
+    b = bits16.int() & 0xFFFF
+    return torch.where(b >= 0x8000, -(b & 0x7FFF), b)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("kp", [16, 80, 1008])
+def test_up_integer_gelu_all_variants(dtype, kp):
+    """z = X W1^T is exact, so hidden must be GELU(z) rounded once: within one unit in the last
+    place of the float64 erf GELU, and within a few FP32 roundings of the rational form."""
+    lib = _lib.load()
+    gen = torch.Generator().manual_seed(kp)
+    mp, hp = 320, 448
+    x = _int_tensor((mp, kp), gen).to(dtype)
+    w1 = _int_tensor((hp, kp), gen).to(dtype)
+    z64 = x.double() @ w1.double().T
+    truth_erf = (0.5 * z64 * torch.special.erfc(-z64 / 2 ** 0.5)).to(dtype)
+    rational = gelu_rational(z64.float()).to(dtype).float()
+    stream = torch.cuda.current_stream().cuda_stream
+    xd, w1d = x.cuda(), w1.cuda()
+    eps = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+    for gelu in ("erf", "rational"):
+        for variant in range(lib.ffn_mi355x_num_variants()):
+            plan = _lib.make_plan(mp, kp, hp, 64, _lib.BF16 if dtype == torch.bfloat16 else _lib.FP16,
+                                  "basic", gelu, 256, variant, -1)
+            hidden = torch.full((mp, hp), float("nan"), dtype=dtype, device="cuda")
+            _lib.check(lib.ffn_mi355x_up(ctypes.byref(plan), xd.data_ptr(), w1d.data_ptr(),
+                                         hidden.data_ptr(), stream))
+            torch.cuda.synchronize()
+            got = hidden.cpu()
+            if gelu == "erf":
+                ulps = (_ordinal(got.view(torch.int16)) - _ordinal(truth_erf.view(torch.int16))).abs()
+                say("up-gelu", dtype, kp, gelu, variant, int(ulps.max()), int((ulps > 0).sum()))
+                assert int(ulps.max()) <= 1, (gelu, variant)
+            else:
+                diff = (got.float() - rational).abs()
+                tol = rational.abs() * eps + 1e-6 * z64.abs().float().clamp(min=1)
+                say("up-gelu", dtype, kp, gelu, variant, float(diff.max()))
+                assert bool((diff <= tol).all()), (gelu, variant)

@@ -1,0 +1,198 @@
+"""CPU tests of the host side: input contract, selection, planning, Stream-K schedule, C ABI.
+
+Restates the reference's CPU tests (validation/test_ffn.py InputTests :24-74 and
+test_selection :172-183) against this package, plus checks of the native plan.
+"""
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from ffn_optim_amd import _lib
+from ffn_optim_amd.cases import (BASELINE_CASES, V1_CASES, case_problem, load_cases,
+                                 make_inputs)
+from ffn_optim_amd.host.dispatch import (DependencyUnavailable, NotApplicable, Selection,
+                                         verify_dependency)
+from ffn_optim_amd.host.inputs import prepare_storage, problem_from_shapes, validate_tensors
+from ffn_optim_amd.host.tiling import make_plan
+from oracle.reference import compare, ffn_torch
+
+REPO = Path(__file__).resolve().parents[1]
+
+
+def test_ranks_and_padding():
+    """validation/test_ffn.py:31-48: padded storage gives the unpadded result, shape restored."""
+    for dtype in (torch.float16, torch.bfloat16):
+        for rank in range(2, 9):
+            shape = (1,) * (rank - 2) + (3, 17)
+            x = torch.randn((*shape[:-1], 34)).to(dtype)[..., ::2]
+            w1 = torch.randn(19, 34).to(dtype)[:, ::2]
+            w2 = torch.randn(23, 38).to(dtype)[:, ::2]
+            p = validate_tensors(x, w1, w2)
+            plan = make_plan(p)
+            xp, a, b, hidden, out, ws = prepare_storage(x, w1, w2, plan)
+            assert xp.shape == (plan.mp, plan.kp) and a.shape == (plan.hp, plan.kp)
+            assert b.shape == (plan.np, plan.hp) and hidden.shape == (plan.mp, plan.hp)
+            assert out.shape == (plan.mp, plan.np) and ws.dtype == torch.float32
+            assert int(xp[p.m:].abs().sum()) == 0 and int(xp[:, p.k:].abs().sum()) == 0
+            got = ffn_torch(xp, a, b, staged=True)[:p.m, :p.n].view(p.output_shape)
+            ref = ffn_torch(x, w1, w2, staged=True)
+            assert compare(got, ref)["passed"]
+            assert got.shape == (*shape[:-1], 23)
+
+
+def test_invalid_shapes():
+    """validation/test_ffn.py:50-59."""
+    p = problem_from_shapes
+    for args in [([3], [4, 3], [3, 4]), ([0, 3], [4, 3], [3, 4]),
+                 ([2, 3], [4, 2], [3, 4]), ([1] * 9, [4, 1], [3, 4]),
+                 ([True, 3], [4, 3], [3, 4]), ([2, 65536], [4, 65536], [3, 4])]:
+        with pytest.raises(ValueError):
+            p(*args)
+    for kwargs in ({"dtype": "float32"}, {"layout": "canonical"}):
+        with pytest.raises(ValueError):
+            p([2, 3], [4, 3], [3, 4], **kwargs)
+
+
+def test_no_device_fallback():
+    """validation/test_ffn.py:61-65: CPU tensors are refused, never computed on the host."""
+    from ffn_optim_amd import ffn
+    with pytest.raises(ValueError, match="requires ROCm GPU"):
+        ffn(torch.zeros(2, 3).half(), torch.zeros(4, 3).half(), torch.zeros(3, 4).half())
+
+
+def test_invalid_tensors():
+    """validation/test_ffn.py:67-74."""
+    x, a, b = torch.zeros(2, 3).half(), torch.zeros(4, 3).half(), torch.zeros(3, 4).half()
+    with pytest.raises(ValueError):
+        validate_tensors(x, a.float(), b)
+    with pytest.raises(ValueError):
+        validate_tensors(x.requires_grad_(), a, b)
+    with pytest.raises(TypeError):
+        validate_tensors(x.detach().numpy(), a, b)
+
+
+def test_selection():
+    """validation/test_ffn.py:172-183 on this plan: full loads unavailable, Stream-K needs a
+    remainder tile for its block_num."""
+    for kind in ("full_load_a", "full_load_b"):
+        with pytest.raises(DependencyUnavailable):
+            Selection(down_impl=kind).require_available()
+        with pytest.raises(DependencyUnavailable):
+            make_plan(problem_from_shapes([64, 128], [256, 128], [64, 256]), Selection(down_impl=kind))
+    with pytest.raises(ValueError):
+        Selection(up_impl="streamk")
+    with pytest.raises(ValueError):
+        Selection(down_impl="splitk")
+    p = problem_from_shapes([64, 128], [256, 128], [64, 256])
+    plan = make_plan(p, Selection(down_impl="streamk"), 8)
+    assert plan.workspace_bytes == plan.native.workspace_bytes > 0
+    assert plan.schedule()["down_sk_tiles"] == 1
+    with pytest.raises(NotApplicable):
+        make_plan(p, Selection(down_impl="streamk"), 1)
+    with pytest.raises(NotApplicable):   # H spans a single K iteration
+        make_plan(problem_from_shapes([64, 128], [64, 128], [64, 64]), Selection(down_impl="streamk"), 8)
+    for bad in (0, 65536, 8.0, True):
+        with pytest.raises(ValueError):
+            make_plan(p, Selection(), bad)
+    assert make_plan(p, Selection(), 8).workspace_shape == (1, 1)
+
+
+def test_baseline_cases_plan_for_both_down_impls():
+    """Every measured workload is plannable for Basic and Stream-K at 256 workgroups."""
+    for case in load_cases(BASELINE_CASES):
+        p = case_problem(case)
+        for down in ("basic", "streamk"):
+            plan = make_plan(p, Selection(down_impl=down), 256)
+            assert plan.mp % 64 == 0 and plan.hp % 64 == 0 and plan.np % 64 == 0 and plan.kp % 16 == 0
+            assert plan.up.bm * plan.up.bn > 0
+
+
+def _sk_start(v, q, r):
+    return v * q + min(v, r)
+
+
+@pytest.mark.parametrize("G", [1, 7, 8, 37, 256])
+def test_streamk_schedule_exact_once_and_slots(G):
+    """The split schedule the kernel follows covers every (tile, K-iteration) exactly once and
+    never needs more partial slots per workgroup than the plan reserves (brute force)."""
+    for (mp, hp, np_) in [(64, 128, 64), (320, 1024, 448), (4096, 4096, 1024), (64, 13824, 5120),
+                          (8192, 12288, 3072), (1024, 3008, 1024)]:
+        for variant in range(_lib.load().ffn_mi355x_num_variants()):
+            try:
+                n = _lib.make_plan(mp, 64, hp, np_, _lib.BF16, "streamk", "erf", G, 0, variant)
+            except ValueError:
+                continue
+            kI, dp, sk = n.down_k_iters, n.down_dp_tiles, n.down_sk_tiles
+            assert dp + sk == n.down_tiles and sk == n.down_tiles % G and sk > 0
+            total = sk * kI
+            q, r = total // G, total % G
+            seen = [[0] * kI for _ in range(sk)]
+            for v in range(G):
+                a, b = _sk_start(v, q, r), _sk_start(v + 1, q, r)
+                tiles = {it // kI for it in range(a, b)}
+                assert len(tiles) <= n.down_slots_per_wg
+                for it in range(a, b):
+                    seen[it // kI][it % kI] += 1
+            assert all(c == 1 for row in seen for c in row)
+            partial = G * n.down_slots_per_wg * n.down_bm * n.down_bn * 4
+            assert n.workspace_bytes >= partial + 4 * sk
+
+
+def test_c_abi_exports_every_declared_symbol():
+    header = (REPO / "include" / "ffn_mi355x.h").read_text()
+    names = set(re.findall(r"^(?:int|const char\*)\s+(ffn_mi355x_\w+)\s*\(", header, re.M))
+    assert len(names) >= 10
+    lib = _lib.load()
+    for name in names:
+        assert hasattr(lib, name), name
+    assert lib.ffn_mi355x_version().decode().startswith("ffn_mi355x gfx950")
+    assert verify_dependency()["version"].startswith("ffn_mi355x gfx950")
+
+
+def test_c_abi_error_codes_without_gpu():
+    """Host-only entry points: argument errors map onto the reference's exception types."""
+    with pytest.raises(ValueError, match="multiples of 64"):
+        _lib.make_plan(100, 64, 64, 64, _lib.BF16, "basic", "erf", 8)
+    with pytest.raises(DependencyUnavailable):
+        _lib.make_plan(64, 64, 64, 64, _lib.BF16, "full_load_b", "erf", 8)
+    with pytest.raises(ValueError, match="block_num"):
+        _lib.make_plan(64, 64, 64, 64, _lib.BF16, "basic", "erf", 0)
+    lib = _lib.load()
+    rc = lib.ffn_mi355x_up(None, None, None, None, None)
+    assert rc == _lib.EINVAL and "invalid plan" in _lib.last_error()
+    info = _lib.variants()
+    assert all(v["lds_bytes"] <= 160 * 1024 and v["waves"] >= 1 for v in info)
+
+
+def test_make_inputs_contract():
+    """common/cases.py:34-50: deterministic, scaled by fan-in, stride-2 and transposed views."""
+    for case in load_cases(BASELINE_CASES)[:1] + load_cases(V1_CASES):
+        x, w1, w2 = make_inputs(case)
+        x2, _, _ = make_inputs(case)
+        assert torch.equal(x, x2)
+        p = case_problem(case)
+        assert tuple(x.shape) == p.input_shape and w1.shape == (p.h, p.k) and w2.shape == (p.n, p.h)
+        if case.get("noncontiguous"):
+            assert x.stride()[-1] == 2 and w1.stride()[-1] == 2
+    case = load_cases(BASELINE_CASES)[0]
+    x, w1, w2 = make_inputs(case)
+    assert abs(x.float().std().item() - 1.0) < 0.02
+    assert abs(w1.float().std().item() * 256 ** 0.5 - 1.0) < 0.02
+    assert abs(w2.float().std().item() * 1024 ** 0.5 - 1.0) < 0.02
+    t = dict(load_cases(BASELINE_CASES)[2], shape=[3, 5, 7, 8], weight1_shape=[9, 8],
+             weight2_shape=[4, 9])
+    xt, _, _ = make_inputs(t)
+    xc, _, _ = make_inputs(dict(t, x_view=None))
+    assert torch.equal(xt, xc) and not xt.is_contiguous() and xt.stride() == (280, 8, 40, 1)
+
+
+def test_case_schema_rejects_bad_files(tmp_path):
+    bad = tmp_path / "c.json"
+    for text in ('{"schema_version": 2, "cases": []}', '{"schema_version": 1, "cases": []}',
+                 '{"schema_version": 1, "cases": [{"case_id": "a", "shape": [2, 3], '
+                 '"weight1_shape": [4, 3], "weight2_shape": [3, 4], "dtype": "float16", "seed": 1.5}]}'):
+        bad.write_text(text)
+        with pytest.raises(ValueError):
+            load_cases(bad)
