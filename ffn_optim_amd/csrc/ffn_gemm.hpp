@@ -42,7 +42,6 @@ struct GemmParams {
     const void* b;        // [N][ldb]   weights (W1 or W2)
     void* c;              // [M][ldc]   hidden or out
     float* ws;            // Stream-K partial-tile slots (FP32)
-    unsigned* counters;   // Stream-K arrivals, one per split tile, zero between launches
     int M, N, K;
     int lda, ldb, ldc;
     int tiles_m, tiles_n;
@@ -129,18 +128,38 @@ __device__ __forceinline__ uint2 pack4(float a, float b, float c, float d) {
 // GELU forms (applied to the FP32 accumulator before the cast)
 // ---------------------------------------------------------------------------
 
-// Exact-form GELU, 0.5*z*(1+erf(z/sqrt(2))) -- torch.nn.functional.gelu(approximate='none') --
-// evaluated as 0.5*z*erfc(-z/sqrt(2)), which is the same function without the cancellation of
-// 1+erf in the negative tail.  erfcf is the ROCm device library's single-precision erfc.
+// Exact-form GELU, z * Phi(z) = 0.5*z*(1+erf(z/sqrt2)) -- F.gelu(approximate='none').
+// Phi is evaluated from erfc of |z|/sqrt2 (no cancellation in either tail):
+//     Phi(z) = 0.5*erfc(|z|/sqrt2)        for z < 0,   1 - 0.5*erfc(|z|/sqrt2)   otherwise,
+// with erfc from the Chebyshev fit of Press, Teukolsky, Vetterling & Flannery, "Numerical
+// Recipes in C" (2nd ed., sec. 6.2, erfcc; fractional error < 1.2e-7 for every x >= 0):
+//     erfc(x) = t*exp(-x*x + P(t)),  t = 1/(1 + x/2),  P a degree-9 polynomial.
+// The factor 1/2 and the change to base 2 are folded into the coefficients, so the whole
+// epilogue is one v_rcp_f32, one v_exp_f32 and about 18 full-rate VALU operations.
 __device__ __forceinline__ float gelu_erf(float z) {
-    return 0.5f * z * erfcf(-z * 0.70710678118654752f);
+    constexpr float L2E = 1.4426950408889634f;                 // log2(e)
+    const float x = __builtin_fabsf(z) * 0.70710678118654752f;  // |z| / sqrt(2)
+    const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.5f, x, 1.0f));
+    float p = __builtin_fmaf(t, 0.17087277f * L2E, -0.82215223f * L2E);
+    p = __builtin_fmaf(t, p, 1.48851587f * L2E);
+    p = __builtin_fmaf(t, p, -1.13520398f * L2E);
+    p = __builtin_fmaf(t, p, 0.27886807f * L2E);
+    p = __builtin_fmaf(t, p, -0.18628806f * L2E);
+    p = __builtin_fmaf(t, p, 0.09678418f * L2E);
+    p = __builtin_fmaf(t, p, 0.37409196f * L2E);
+    p = __builtin_fmaf(t, p, 1.00002368f * L2E);
+    p = __builtin_fmaf(t, p, -1.26551223f * L2E - 1.0f);      // -1: the factor 1/2 of Phi
+    const float half = t * __builtin_amdgcn_exp2f(__builtin_fmaf(-x, x * L2E, p));
+    const float phi = z < 0.0f ? half : 1.0f - half;
+    return z * phi;
 }
 
 // Rational erf GELU: t = clamp(z/sqrt2, +-3.92), erf(t) ~ t*P5(t^2)/Q5(t^2), coefficients and
-// operation order of validation/reference.py:5-13 (= ops/kernel/ffn.py:548-572).
+// operation order of validation/reference.py:5-13 (= ops/kernel/ffn.py:548-572); the division
+// is a v_rcp_f32 (1 ulp) and a multiply.
 __device__ __forceinline__ float gelu_rational(float z) {
     float t = z * 0.70710678118654752f;
-    t = fminf(fmaxf(t, -3.92f), 3.92f);
+    t = __builtin_fminf(__builtin_fmaxf(t, -3.92f), 3.92f);
     const float t2 = t * t;
     float p = t2 * 0.053443748819f + 7.5517016694f;
     p = p * t2 + 101.62808918f;
@@ -175,21 +194,89 @@ __device__ __forceinline__ void tile_coords(const GemmParams& p, int t, int& tm,
     tn = r / rows;
 }
 
+// Split-region bookkeeping: split iteration x (0-based inside the split region) belongs to
+// workgroup sk_owner(x); workgroup v starts at sk_start(v).
+__device__ __forceinline__ int sk_owner(const GemmParams& p, int x) {
+    if (p.sk_q == 0) return x;
+    const int big = (p.sk_q + 1) * p.sk_r;
+    if (x < big) return x / (p.sk_q + 1);
+    return p.sk_r + (x - big) / p.sk_q;
+}
+__device__ __forceinline__ int sk_start(const GemmParams& p, int v) {
+    return v * p.sk_q + min(v, p.sk_r);
+}
+__device__ __forceinline__ float* sk_slot(const GemmParams& p, int v, int local, int tile_elems) {
+    return p.ws + ((size_t)v * p.slots_per_wg + local) * (size_t)tile_elems;
+}
+
+// One unit of work of a workgroup: K-iterations [kb, ke) of tile (tm, tn).  `split` >= 0 marks
+// a Stream-K piece of split tile `split` that shares the tile with other workgroups and goes
+// to partial slot `local` of this workgroup.
+struct Unit {
+    int tm, tn, kb, ke;
+    int split, local;
+    bool valid;
+};
+
+// Walks the units of virtual workgroup v: whole tiles v, v+G, ... below dp_tiles, then (for
+// Stream-K) its contiguous range of split iterations cut at tile boundaries.
+template <bool SK>
+struct UnitWalker {
+    int G, v, dp_next, it, it_begin, it_end;
+    __device__ __forceinline__ UnitWalker(const GemmParams& p, int v_, int G_) : G(G_), v(v_) {
+        dp_next = v;
+        it_begin = it_end = it = 0;
+        if constexpr (SK) {
+            it_begin = it = sk_start(p, v);
+            it_end = sk_start(p, v + 1);
+        }
+    }
+    __device__ __forceinline__ Unit next(const GemmParams& p) {
+        Unit u;
+        u.valid = false;
+        u.split = -1;
+        u.local = 0;
+        if (dp_next < p.dp_tiles) {
+            tile_coords(p, dp_next, u.tm, u.tn);
+            u.kb = 0, u.ke = p.k_iters, u.valid = true;
+            dp_next += G;
+            return u;
+        }
+        if constexpr (SK) {
+            if (it < it_end) {
+                const int kI = p.k_iters;
+                const int s = it / kI;
+                u.kb = it - s * kI;
+                u.ke = min(kI, u.kb + (it_end - it));
+                tile_coords(p, p.dp_tiles + s, u.tm, u.tn);
+                const bool shared = sk_owner(p, s * kI) != sk_owner(p, s * kI + kI - 1);
+                u.split = shared ? s : -1;
+                u.local = s - it_begin / kI;
+                u.valid = true;
+                it += u.ke - u.kb;
+            }
+        }
+        return u;
+    }
+};
+
 // ---------------------------------------------------------------------------
 // the GEMM engine
 // ---------------------------------------------------------------------------
 
 template <int DT, class C>
 struct Engine {
-    static constexpr int FM = C::FM, FN = C::FN, NT = C::NT;
+    static constexpr int FM = C::FM, FN = C::FN, NT = C::NT, S = C::STAGES, KS = C::KSTEPS;
+    static_assert(KS % 2 == 0, "fragment double-buffer assumes an even number of k-steps");
 
     lds_char* smem;
     int tid, lane, wave, wm, wn;
-    // per-lane LDS byte offsets of the fragment rows (without stage / k-step parts)
-    int a_row_off, b_row_off;
-    int swz;  // chunk XOR of this lane's fragment rows
+    int a_row_off, b_row_off;  // per-lane LDS byte offsets of the fragment rows
+    int swz;                   // chunk XOR of this lane's fragment rows
+    int dma_a, dma_b;          // per-lane DMA source offsets inside a block (without k0)
+    int dma_k;                 // K element of this lane's DMA chunk (without k0)
 
-    __device__ __forceinline__ Engine(lds_char* s) : smem(s) {
+    __device__ __forceinline__ Engine(lds_char* s, const GemmParams& p) : smem(s) {
         tid = threadIdx.x;
         lane = tid & 63;
         wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -199,108 +286,230 @@ struct Engine {
         a_row_off = (wm * C::WTM + r) * C::ROWB;
         b_row_off = C::A_BYTES + (wn * C::WTN + r) * C::ROWB;
         swz = (r / C::RPL) % C::CH;
+        // DMA: this lane fills physical chunk (lane % CH) of row (lane / CH) of each 1 KiB block,
+        // i.e. logical chunk pc ^ swz(row); the swizzle depends only on the row inside the block.
+        const int rl = lane / C::CH, pc = lane % C::CH;
+        dma_k = (pc ^ ((rl / C::RPL) % C::CH)) * 8;
+        dma_a = rl * p.lda * 2 + dma_k * 2;
+        dma_b = rl * p.ldb * 2 + dma_k * 2;
     }
 
-    // Per-lane part of the DMA source offset: this lane fills physical chunk (lane % CH) of
-    // row (lane / CH) of every 1 KiB block, i.e. logical chunk c = pc ^ swz(row).  The swizzle
-    // of a row depends only on its position inside the block, so one lane offset per operand
-    // serves every block; the block's row offset is added to it.  The whole offset stays in
-    // the VGPR operand: the buffer range check covers voffset but not soffset.
-    __device__ __forceinline__ int dma_chunk() const {
-        const int rl = lane / C::CH;
-        const int pc = lane % C::CH;
-        return pc ^ ((rl / C::RPL) % C::CH);
+    __device__ __forceinline__ void rsrc(const GemmParams& p, const Unit& u,
+                                         __amdgpu_buffer_rsrc_t& ra, __amdgpu_buffer_rsrc_t& rb) const {
+        const int row0 = u.tm * C::BM, col0 = u.tn * C::BN;
+        const int lda2 = p.lda * 2, ldb2 = p.ldb * 2;
+        const char* abase = (const char*)p.a + (size_t)row0 * (size_t)lda2;
+        const char* bbase = (const char*)p.b + (size_t)col0 * (size_t)ldb2;
+        ra = make_rsrc(abase, (uint32_t)min(C::BM, p.M - row0) * (uint32_t)lda2);
+        rb = make_rsrc(bbase, (uint32_t)min(C::BN, p.N - col0) * (uint32_t)ldb2);
     }
 
-    // Issue the DMA of K-iteration `kit` into LDS stage `stage`.  Rows past the operand and
-    // chunks past K get an offset >= 2^31, beyond any range, and read as zero.
-    __device__ __forceinline__ void issue(const __amdgpu_buffer_rsrc_t& ra,
-                                          const __amdgpu_buffer_rsrc_t& rb, int lda2, int ldb2,
-                                          int K, int stage, int kit) {
+    // DMA source offsets of this lane for K-iteration `kit`.  Chunks past K get an offset
+    // >= 2^31, beyond any range, and read as zero (rows past the operand are out of range of
+    // the tile's descriptor).  The whole offset travels in the VGPR operand: the buffer range
+    // check covers voffset but not soffset.
+    __device__ __forceinline__ void dma_offsets(const GemmParams& p, int kit, uint32_t& va,
+                                                uint32_t& vb) const {
         const int k0 = kit * C::BK;
+        const bool ok = (k0 + C::BK <= p.K) || (k0 + dma_k < p.K);
+        va = ok ? (uint32_t)(dma_a + k0 * 2) : 0x80000000u;
+        vb = ok ? (uint32_t)(dma_b + k0 * 2) : 0x80000000u;
+    }
+
+    // DMA instruction D (of the LOADS this wave issues per stage) into LDS stage `stage`.
+    template <int D>
+    __device__ __forceinline__ void issue_one(const GemmParams& p, const __amdgpu_buffer_rsrc_t& ra,
+                                              const __amdgpu_buffer_rsrc_t& rb, int stage,
+                                              uint32_t va, uint32_t vb) const {
         lds_char* st = smem + stage * C::STAGE_BYTES;
-        const int rl = lane / C::CH;
-        const int kk = k0 + dma_chunk() * 8;
-        const bool ok = (k0 + C::BK <= K) || (kk < K);
-        const uint32_t va = ok ? (uint32_t)(rl * lda2 + kk * 2) : 0x80000000u;
-        const uint32_t vb = ok ? (uint32_t)(rl * ldb2 + kk * 2) : 0x80000000u;
-#pragma unroll
-        for (int i = 0; i < C::A_PW; ++i) {
-            const int blk = wave * C::A_PW + i;
+        if constexpr (D < C::A_PW) {
+            const int blk = wave * C::A_PW + D;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 ra, (__attribute__((address_space(3))) void*)(st + blk * 1024), 16,
-                (int)(va + (uint32_t)(blk * C::RPB * lda2)), 0, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < C::B_PW; ++i) {
-            const int blk = wave * C::B_PW + i;
+                (int)(va + (uint32_t)blk * (uint32_t)(C::RPB * p.lda * 2)), 0, 0, 0);
+        } else {
+            const int blk = wave * C::B_PW + (D - C::A_PW);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rb, (__attribute__((address_space(3))) void*)(st + C::A_BYTES + blk * 1024), 16,
-                (int)(vb + (uint32_t)(blk * C::RPB * ldb2)), 0, 0, 0);
+                (int)(vb + (uint32_t)blk * (uint32_t)(C::RPB * p.ldb * 2)), 0, 0, 0);
         }
     }
 
-    __device__ __forceinline__ void compute(int stage, f32x16 (&acc)[FN][FM]) {
+    template <int D0, int D1>
+    __device__ __forceinline__ void issue_range(const GemmParams& p, const __amdgpu_buffer_rsrc_t& ra,
+                                                const __amdgpu_buffer_rsrc_t& rb, int stage,
+                                                uint32_t va, uint32_t vb) const {
+        if constexpr (D0 < D1) {
+            issue_one<D0>(p, ra, rb, stage, va, vb);
+            issue_range<D0 + 1, D1>(p, ra, rb, stage, va, vb);
+        }
+    }
+
+    // The first min(S-1, n) K-iterations of a unit go to stages 0, 1, ...; iteration S-1+it is
+    // fetched during iteration it.
+    __device__ __forceinline__ void prologue(const GemmParams& p, const Unit& u) const {
+        __amdgpu_buffer_rsrc_t ra, rb;
+        rsrc(p, u, ra, rb);
+#pragma unroll
+        for (int s = 0; s < S - 1; ++s)
+            if (u.kb + s < u.ke) {
+                uint32_t va, vb;
+                dma_offsets(p, u.kb + s, va, vb);
+                issue_range<0, C::LOADS>(p, ra, rb, s, va, vb);
+            }
+    }
+
+    // Fragment registers: A (activation rows) double-buffered across k-steps, B (weight rows)
+    // reloaded in place right after its last use, which the j-major MFMA order makes early.
+    u32x4 fa[2][FM], fb[FN];
+
+    __device__ __forceinline__ int frag_chunk(int ks) const {
+        return ((2 * ks + (lane >> 5)) ^ swz) * 16;
+    }
+    template <int BUF, int I>
+    __device__ __forceinline__ void read_a(int stage, int ks) {
         const lds_char* st = smem + stage * C::STAGE_BYTES;
-#pragma unroll
-        for (int s = 0; s < C::KSTEPS; ++s) {
-            const int chunk = ((2 * s + (lane >> 5)) ^ swz) * 16;
-            u32x4 af[FM], bf[FN];
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-                af[i] = *(const __attribute__((address_space(3))) u32x4*)(st + a_row_off + i * 32 * C::ROWB + chunk);
-#pragma unroll
-            for (int j = 0; j < FN; ++j)
-                bf[j] = *(const __attribute__((address_space(3))) u32x4*)(st + b_row_off + j * 32 * C::ROWB + chunk);
-#pragma unroll
-            for (int j = 0; j < FN; ++j)
-#pragma unroll
-                for (int i = 0; i < FM; ++i) acc[j][i] = mfma32<DT>(bf[j], af[i], acc[j][i]);
+        fa[BUF][I] = *(const __attribute__((address_space(3))) u32x4*)(st + a_row_off + I * 32 * C::ROWB + frag_chunk(ks));
+    }
+    template <int J>
+    __device__ __forceinline__ void read_b(int stage, int ks) {
+        const lds_char* st = smem + stage * C::STAGE_BYTES;
+        fb[J] = *(const __attribute__((address_space(3))) u32x4*)(st + b_row_off + J * 32 * C::ROWB + frag_chunk(ks));
+    }
+    template <int BUF, int I0, int I1>
+    __device__ __forceinline__ void read_a_range(int stage, int ks) {
+        if constexpr (I0 < I1) {
+            read_a<BUF, I0>(stage, ks);
+            read_a_range<BUF, I0 + 1, I1>(stage, ks);
+        }
+    }
+    template <int J0, int J1>
+    __device__ __forceinline__ void read_b_range(int stage, int ks) {
+        if constexpr (J0 < J1) {
+            read_b<J0>(stage, ks);
+            read_b_range<J0 + 1, J1>(stage, ks);
         }
     }
 
-    // acc = sum over K-iterations [kb, ke) of tile (tm, tn).
-    __device__ __forceinline__ void mainloop(const GemmParams& p, int tm, int tn, int kb, int ke,
+    __device__ __forceinline__ void barrier() const {
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS reads are done
+        __builtin_amdgcn_s_barrier();
+    }
+
+    // ---- one k-step, scheduled by hand ------------------------------------------------------
+    // The FN*FM MFMAs of A-buffer CB are issued one per slot in j-major order; between them go
+    // the fragment reads of the next k-step (MODE 0: same stage; MODE 1: after the stage wait +
+    // barrier, k-step 0 of the next stage; MODE 2: after a barrier, the DMA prologue of the
+    // next unit) and this slot's share of the refill DMA.  sched_barrier fences keep the
+    // compiler from regrouping them: a burst of DMA instructions fills the texture-address FIFO
+    // and stalls the in-order issue of the MFMAs behind it.
+    static constexpr int NM = FN * FM;
+    // slot of the last k-step after whose MFMA the stage wait + barrier is placed: the end of
+    // the j = 0 block, from where every B fragment can be reloaded after its last use
+    static constexpr int SYNC_Q = FM - 1;
+    // Slots carrying the refill DMA.  With two stages the data is waited for at the end of the
+    // same iteration, so it goes out in the first half; with more, it is spread over every slot
+    // before the stage wait (whose count assumes whole groups issued).
+    static constexpr int DMA_SLOTS = (S == 2) ? (KS / 2) * NM : (KS - 1) * NM + SYNC_Q;
+    static_assert(KS >= 2 && DMA_SLOTS >= 1, "at least two k-steps per stage");
+
+    template <int CB, int MODE, bool DMA, int KSI, int Q>
+    __device__ __forceinline__ void slot(const GemmParams& p, f32x16 (&acc)[FN][FM], int cur, int nxt,
+                                         const __amdgpu_buffer_rsrc_t& ra, const __amdgpu_buffer_rsrc_t& rb,
+                                         int dma_stage, uint32_t va, uint32_t vb, const Unit& nx) {
+        constexpr int j = Q / FM, i = Q % FM;
+        acc[j][i] = mfma32<DT>(fb[j], fa[CB][i], acc[j][i]);
+        constexpr int NB = 1 - CB;
+        if constexpr (MODE == 0) {
+            // A fragments of the next k-step over the first half of the slots; B fragment j
+            // right after its last use (the end of block j)
+            constexpr int half = NM / 2 > 0 ? NM / 2 : 1;
+            constexpr int a0 = Q * FM / half, a1 = (Q + 1) * FM / half;
+            if constexpr (Q < half) read_a_range<NB, a0, (a1 < FM ? a1 : FM)>(cur, KSI + 1);
+            if constexpr (i == FM - 1) read_b<j>(cur, KSI + 1);
+        } else {
+            if constexpr (Q == SYNC_Q) {
+                if constexpr (MODE == 1) {
+                    // every wave's DMA of the next stage has landed; every wave is done with the
+                    // stage the next refill overwrites
+                    wait_vmcnt<C::LOADS * (S - 2)>();
+                    barrier();
+                } else if (nx.valid) {
+                    barrier();
+                    prologue(p, nx);
+                }
+            }
+            if constexpr (MODE == 1 && Q >= SYNC_Q) {
+                constexpr int span = NM - SYNC_Q, qq = Q - SYNC_Q;
+                constexpr int a0 = qq * FM / span, a1 = (qq + 1) * FM / span;
+                read_a_range<NB, a0, a1>(nxt, 0);
+                if constexpr (i == FM - 1) read_b<j>(nxt, 0);
+            }
+        }
+        constexpr int g = KSI * NM + Q;  // this slot's share of the refill DMA
+        if constexpr (DMA && g < DMA_SLOTS && (KSI + 1 < KS || Q < SYNC_Q)) {
+            constexpr int t0 = g * C::LOADS / DMA_SLOTS, t1 = (g + 1) * C::LOADS / DMA_SLOTS;
+            issue_range<t0, t1>(p, ra, rb, dma_stage, va, vb);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    template <int CB, int MODE, bool DMA, int KSI, int Q>
+    __device__ __forceinline__ void slots(const GemmParams& p, f32x16 (&acc)[FN][FM], int cur, int nxt,
+                                          const __amdgpu_buffer_rsrc_t& ra, const __amdgpu_buffer_rsrc_t& rb,
+                                          int dma_stage, uint32_t va, uint32_t vb, const Unit& nx) {
+        if constexpr (Q < NM) {
+            slot<CB, MODE, DMA, KSI, Q>(p, acc, cur, nxt, ra, rb, dma_stage, va, vb, nx);
+            slots<CB, MODE, DMA, KSI, Q + 1>(p, acc, cur, nxt, ra, rb, dma_stage, va, vb, nx);
+        }
+    }
+
+    template <bool LAST, int KSI>
+    __device__ __forceinline__ void ksteps(const GemmParams& p, const Unit& nx,
+                                           const __amdgpu_buffer_rsrc_t& ra,
+                                           const __amdgpu_buffer_rsrc_t& rb, int cur, int dstage,
+                                           uint32_t va, uint32_t vb, f32x16 (&acc)[FN][FM]) {
+        if constexpr (KSI < KS) {
+            constexpr int MODE = (KSI + 1 < KS) ? 0 : (LAST ? 2 : 1);
+            const int nxt = (cur + 1 == S) ? 0 : cur + 1;
+            // the last iteration of a unit refills nothing (its DMA prologue for the next unit
+            // is issued after the barrier of its last k-step)
+            slots<KSI & 1, MODE, !LAST, KSI, 0>(p, acc, cur, nxt, ra, rb, dstage, va, vb, nx);
+            ksteps<LAST, KSI + 1>(p, nx, ra, rb, cur, dstage, va, vb, acc);
+        }
+    }
+
+    // acc = sum over K-iterations [u.kb, u.ke) of tile (u.tm, u.tn).  On entry the DMA prologue
+    // of the unit is in flight, possibly behind the previous unit's stores, so the first wait
+    // drains everything.  Iteration it fetches iteration it+S-1 into the stage freed at the end
+    // of it-1; past the end of the unit it issues the same DMA against an empty descriptor
+    // (zeros into the free stage), which keeps every stage wait a compile-time count.  The
+    // last iteration starts the DMA prologue of `nx`, which then overlaps this unit's epilogue.
+    __device__ __forceinline__ void mainloop(const GemmParams& p, const Unit& u, const Unit& nx,
                                              f32x16 (&acc)[FN][FM]) {
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int i = 0; i < FM; ++i) acc[j][i] = f32x16{};
-
-        const int row0 = tm * C::BM, col0 = tn * C::BN;
-        const int lda2 = p.lda * 2, ldb2 = p.ldb * 2;
-        const char* abase = (const char*)p.a + (size_t)row0 * (size_t)lda2;
-        const char* bbase = (const char*)p.b + (size_t)col0 * (size_t)ldb2;
-        const uint32_t abytes = (uint32_t)min(C::BM, p.M - row0) * (uint32_t)lda2;
-        const uint32_t bbytes = (uint32_t)min(C::BN, p.N - col0) * (uint32_t)ldb2;
-        const __amdgpu_buffer_rsrc_t ra = make_rsrc(abase, abytes);
-        const __amdgpu_buffer_rsrc_t rb = make_rsrc(bbase, bbytes);
-
-        // no wave may still be reading LDS from the previous unit
-        __syncthreads();
-#pragma unroll
-        for (int s = 0; s < C::STAGES - 1; ++s)
-            if (kb + s < ke) issue(ra, rb, lda2, ldb2, p.K, s, kb + s);
-
-        int stage = 0;
-        for (int kit = kb; kit < ke; ++kit) {
-            if constexpr (C::STAGES == 2) {
-                wait_vmcnt<0>();
-            } else {
-                static_assert(C::STAGES == 3, "2 or 3 LDS stages");
-                if (kit + 1 < ke) wait_vmcnt<C::LOADS>();
-                else wait_vmcnt<0>();
-            }
-            __syncthreads();
-            const int nk = kit + C::STAGES - 1;
-            if (nk < ke) {
-                int ns = stage + C::STAGES - 1;
-                if (ns >= C::STAGES) ns -= C::STAGES;
-                issue(ra, rb, lda2, ldb2, p.K, ns, nk);
-            }
-            compute(stage, acc);
-            stage = (stage + 1 == C::STAGES) ? 0 : stage + 1;
+        __amdgpu_buffer_rsrc_t ra, rb;
+        rsrc(p, u, ra, rb);
+        const __amdgpu_buffer_rsrc_t rnull = make_rsrc(p.a, 0);
+        const int n = u.ke - u.kb;
+        wait_vmcnt<0>();
+        barrier();
+        read_a_range<0, 0, FM>(0, 0);
+        read_b_range<0, FN>(0, 0);
+        int cur = 0;
+        for (int it = 0; it < n - 1; ++it) {
+            const int dkit = it + S - 1;
+            const bool real = dkit < n;
+            uint32_t va, vb;
+            dma_offsets(p, u.kb + dkit, va, vb);
+            const int dstage = (cur == 0) ? S - 1 : cur - 1;
+            ksteps<false, 0>(p, nx, real ? ra : rnull, real ? rb : rnull, cur, dstage, va, vb, acc);
+            cur = (cur + 1 == S) ? 0 : cur + 1;
         }
+        ksteps<true, 0>(p, nx, ra, rb, cur, 0, 0u, 0u, acc);
     }
 
     // Output position of accumulator group (j, i, q): row m, columns n..n+3.
@@ -320,14 +529,16 @@ struct Engine {
         }
     }
 
-    // Write acc (activated, cast) to C[tile] with row/column masking.
+    // Write acc (activated, cast) to C[tile] with row/column masking.  One 32x32 block at a
+    // time: the scheduling fences keep the compiler from moving all 256 accumulators into
+    // VGPRs at once (which would spill the long-lived addressing registers).
     template <int EPI>
     __device__ __forceinline__ void store_tile(const GemmParams& p, int tm, int tn,
                                                f32x16 (&acc)[FN][FM]) const {
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
-            for (int i = 0; i < FM; ++i)
+            for (int i = 0; i < FM; ++i) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     int m, n;
@@ -335,6 +546,8 @@ struct Engine {
                     store4<EPI>(p, m, n, acc[j][i][4 * q], acc[j][i][4 * q + 1],
                                 acc[j][i][4 * q + 2], acc[j][i][4 * q + 3]);
                 }
+                __builtin_amdgcn_sched_barrier(0);
+            }
     }
 
     // FP32 partial tile in the accumulator's own register order: group (j, i, q) of thread
@@ -350,29 +563,18 @@ struct Engine {
                     const f32x4 v = {acc[j][i][4 * q], acc[j][i][4 * q + 1], acc[j][i][4 * q + 2],
                                      acc[j][i][4 * q + 3]};
                     *(f32x4*)(slot + ((size_t)idx * NT + tid) * 4) = v;
+                    if (q == 3) __builtin_amdgcn_sched_barrier(0);
                 }
     }
 };
 
-// Split-region bookkeeping: iteration x (0-based inside the split region) belongs to
-// workgroup sk_owner(x); workgroup v starts at sk_start(v).
-__device__ __forceinline__ int sk_owner(const GemmParams& p, int x) {
-    if (p.sk_q == 0) return x;
-    const int big = (p.sk_q + 1) * p.sk_r;
-    if (x < big) return x / (p.sk_q + 1);
-    return p.sk_r + (x - big) / p.sk_q;
-}
-__device__ __forceinline__ int sk_start(const GemmParams& p, int v) {
-    return v * p.sk_q + min(v, p.sk_r);
-}
-__device__ __forceinline__ float* sk_slot(const GemmParams& p, int v, int local, int tile_elems) {
-    return p.ws + ((size_t)v * p.slots_per_wg + local) * (size_t)tile_elems;
-}
-
+// Persistent GEMM: every workgroup walks its units (whole tiles, then for Stream-K its split
+// iterations) with the DMA of the next unit overlapping the epilogue of the current one.
+// Split pieces that share a tile publish FP32 partials; ffn_sk_reduce_kernel finishes them.
 template <int DT, class C, int EPI, bool SK>
 __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
     __shared__ __attribute__((aligned(1024))) char smem_raw[C::LDS_BYTES];
-    Engine<DT, C> eng((lds_char*)smem_raw);
+    Engine<DT, C> eng((lds_char*)smem_raw, p);
     f32x16 acc[C::FN][C::FM];
 
     const int G = gridDim.x;
@@ -381,65 +583,51 @@ __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
     // consecutive virtual ids (which take neighbouring tiles) share one XCD's L2.
     const int v = ((G & 7) == 0) ? (g & 7) * (G >> 3) + (g >> 3) : g;
 
-    for (int t = v; t < p.dp_tiles; t += G) {
-        int tm, tn;
-        tile_coords(p, t, tm, tn);
-        eng.mainloop(p, tm, tn, 0, p.k_iters, acc);
-        eng.template store_tile<EPI>(p, tm, tn, acc);
+    UnitWalker<SK> walk(p, v, G);
+    Unit u = walk.next(p);
+    if (!u.valid) return;
+    eng.prologue(p, u);
+    while (true) {
+        const Unit nx = walk.next(p);
+        eng.mainloop(p, u, nx, acc);
+        if (SK && u.split >= 0)
+            eng.store_partial(sk_slot(p, v, u.local, C::BM * C::BN), acc);
+        else
+            eng.template store_tile<EPI>(p, u.tm, u.tn, acc);
+        if (!nx.valid) break;
+        u = nx;
     }
+}
 
-    if constexpr (SK) {
-        // Stream-K region: this workgroup owns split iterations [it_begin, it_end), which may
-        // cover the tail of one tile, whole tiles and the head of another.  A tile reduced by
-        // one workgroup is stored directly.  Otherwise every contributor publishes an FP32
-        // partial and counts its arrival; the last to arrive sums all partials in ascending
-        // K order (so the result does not depend on arrival order), rounds once to the
-        // storage type and re-arms the counter.  Nobody waits on anybody: no co-residency
-        // assumption, every workgroup runs to completion.
-        __shared__ int last_flag;
-        constexpr int TE = C::BM * C::BN;
-        const int kI = p.k_iters;
-        const int it_begin = sk_start(p, v), it_end = sk_start(p, v + 1);
-        for (int it = it_begin; it < it_end;) {
-            const int s = it / kI;
-            const int kb = it - s * kI;
-            const int ke = min(kI, kb + (it_end - it));
-            const int t = p.dp_tiles + s;
-            int tm, tn;
-            tile_coords(p, t, tm, tn);
-            eng.mainloop(p, tm, tn, kb, ke, acc);
-            const int first = sk_owner(p, s * kI), last = sk_owner(p, s * kI + kI - 1);
-            if (first == last) {
-                eng.template store_tile<EPI>(p, tm, tn, acc);
-            } else {
-                eng.store_partial(sk_slot(p, v, s - it_begin / kI, TE), acc);
-                __threadfence();
-                __syncthreads();
-                if (eng.tid == 0) {
-                    const unsigned old = __hip_atomic_fetch_add(
-                        p.counters + s, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-                    last_flag = (old == (unsigned)(last - first));
-                }
-                __syncthreads();
-                if (last_flag) {
-                    __threadfence();
-                    for (int j = 0; j < C::FN; ++j)
-                        for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-                            for (int q = 0; q < 4; ++q) {
-                                const size_t off = ((size_t)((j * C::FM + i) * 4 + q) * C::NT + eng.tid) * 4;
-                                f32x4 tot = *(const f32x4*)(sk_slot(p, first, s - sk_start(p, first) / kI, TE) + off);
-                                for (int w = first + 1; w <= last; ++w)
-                                    tot += *(const f32x4*)(sk_slot(p, w, s - sk_start(p, w) / kI, TE) + off);
-                                int m, n;
-                                eng.group_pos(tm, tn, j, i, q, m, n);
-                                eng.template store4<EPI>(p, m, n, tot.x, tot.y, tot.z, tot.w);
-                            }
-                    if (eng.tid == 0)
-                        __hip_atomic_store(p.counters + s, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-            }
-            it += ke - kb;
+// Stream-K fixup, stream-ordered after ffn_gemm_kernel<..., true>: workgroup (s, r) sums the
+// FP32 partials of split tile s in ascending K order (independent of which workgroup finished
+// first), rounds once to the storage type and stores.  r selects a slice of the tile.
+template <int DT, class C>
+__global__ void __launch_bounds__(C::NT) ffn_sk_reduce_kernel(GemmParams p, int slices) {
+    constexpr int TE = C::BM * C::BN;
+    constexpr int GROUPS = C::FN * C::FM * 4;
+    const int s = blockIdx.x / slices, r = blockIdx.x - s * slices;
+    const int kI = p.k_iters;
+    const int first = sk_owner(p, s * kI), last = sk_owner(p, s * kI + kI - 1);
+    if (first == last) return;  // stored whole by its only contributor
+    int tm, tn;
+    tile_coords(p, p.dp_tiles + s, tm, tn);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave % C::WGM, wn = wave / C::WGM;
+    const int per = (GROUPS + slices - 1) / slices;
+    const int g0 = r * per, g1 = min(GROUPS, g0 + per);
+    for (int idx = g0; idx < g1; ++idx) {
+        const int q = idx & 3, ji = idx >> 2;
+        const int j = ji / C::FM, i = ji - j * C::FM;
+        const size_t off = ((size_t)idx * C::NT + tid) * 4;
+        f32x4 tot = *(const f32x4*)(sk_slot(p, first, s - sk_start(p, first) / kI, TE) + off);
+        for (int w = first + 1; w <= last; ++w)
+            tot += *(const f32x4*)(sk_slot(p, w, s - sk_start(p, w) / kI, TE) + off);
+        const int m = tm * C::BM + wm * C::WTM + 32 * i + (lane & 31);
+        const int n = tn * C::BN + wn * C::WTN + 32 * j + 8 * q + 4 * (lane >> 5);
+        if (m < p.M && n < p.N) {
+            const uint2 v = pack4<DT>(tot.x, tot.y, tot.z, tot.w);
+            *(uint2*)((char*)p.c + ((size_t)m * (size_t)p.ldc + (size_t)n) * 2) = v;
         }
     }
 }

@@ -244,9 +244,7 @@ int ffn_mi355x_make_plan(int mp, int kp, int hp, int np, int dtype, int down_imp
         plan->down_sk_tiles = (int)s.sk;
         plan->down_slots_per_wg = (int)s.slots;
         plan->down_grid = G;
-        const size_t partials = (size_t)G * (size_t)s.slots * (size_t)D.bm * (size_t)D.bn * 4u;
-        const size_t counters = ((size_t)s.sk * 4u + 255u) / 256u * 256u;
-        plan->workspace_bytes = partials + counters;
+        plan->workspace_bytes = (size_t)G * (size_t)s.slots * (size_t)D.bm * (size_t)D.bn * 4u;
     } else {
         plan->down_dp_tiles = plan->down_tiles;
         plan->down_grid = plan->down_tiles < G ? plan->down_tiles : G;
@@ -302,7 +300,6 @@ int ffn_mi355x_down(const ffn_mi355x_plan* plan, const void* hidden, const void*
         gp.sk_r = (int)(total % G);
         gp.slots_per_wg = plan->down_slots_per_wg;
         gp.ws = (float*)ws;
-        gp.counters = (unsigned*)((char*)ws + (size_t)G * plan->down_slots_per_wg * D.bm * D.bn * 4u);
         return launch(D, plan->dtype, FFN_ROLE_DOWN_STREAMK, gp, G, hip_stream);
     }
     gp.dp_tiles = plan->down_tiles;

@@ -11,9 +11,10 @@
     X(2, 128, 256, 64, 2, 2, 3)         \
     X(3, 128, 128, 64, 2, 2, 2)         \
     X(4, 64, 64, 64, 2, 2, 2)           \
-    X(5, 64, 128, 64, 2, 2, 3)
+    X(5, 64, 128, 64, 2, 2, 3)          \
+    X(6, 256, 256, 32, 2, 2, 4)
 
-#define FFN_NUM_VARIANTS 6
+#define FFN_NUM_VARIANTS 7
 
 // launch roles of one variant
 enum { FFN_ROLE_UP_ERF = 0, FFN_ROLE_UP_RATIONAL = 1, FFN_ROLE_DOWN_BASIC = 2, FFN_ROLE_DOWN_STREAMK = 3 };

@@ -86,8 +86,8 @@ def validate_tensors(x, weight1, weight2, layout="linear", require_device=False)
 def prepare_storage(x, weight1, weight2, plan):
     """Contiguise and zero-pad into [mp,kp], [hp,kp], [np,hp]; allocate hidden, out, workspace.
 
-    Same buffers as ops/host/inputs.py:74-90.  The workspace is zero-filled: the
-    Stream-K arrival counters it holds must start at zero (the kernel re-arms them).
+    Same buffers as ops/host/inputs.py:74-90; the FP32 workspace holds the Stream-K
+    partial tiles (every slot is written before it is read).
     """
     import torch
 
@@ -102,5 +102,5 @@ def prepare_storage(x, weight1, weight2, plan):
     w2p[:p.n, :p.h].copy_(w2c)
     hidden = torch.empty((plan.mp, plan.hp), device=x.device, dtype=x.dtype)
     out = torch.empty((plan.mp, plan.np), device=x.device, dtype=x.dtype)
-    ws = torch.zeros(plan.workspace_shape, device=x.device, dtype=torch.float32)
+    ws = torch.empty(plan.workspace_shape, device=x.device, dtype=torch.float32)
     return xp, w1p, w2p, hidden, out, ws

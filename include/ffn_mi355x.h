@@ -61,7 +61,7 @@ typedef struct ffn_mi355x_plan {
     int down_dp_tiles;           /* tiles reduced whole by one workgroup */
     int down_sk_tiles;           /* tiles whose H-range is split over workgroups */
     int down_slots_per_wg;       /* FP32 partial-tile slots per workgroup */
-    size_t workspace_bytes;      /* FP32 partials + per-tile arrival counters */
+    size_t workspace_bytes;      /* FP32 partial-tile slots of the Stream-K down */
 } ffn_mi355x_plan;
 
 /* Device check replacing the Ascend950/AIC checks of ops/api.py:58-66:
@@ -86,8 +86,9 @@ int ffn_mi355x_workspace_bytes(const ffn_mi355x_plan* plan, size_t* bytes);
  * dtype, then the Basic or Stream-K down GEMM writing `out` [mp,np].  Replaces
  * the single artifact(*tensors, block_num) launch of ops/api.py:43 built by
  * compile_kernel (ops/host/dispatch.py:97-116) from ops/kernel/ffn.py.
- * `ws` must hold plan->workspace_bytes and be zeroed once before first use;
- * the Stream-K kernel leaves its arrival counters at zero again on exit. */
+ * `ws` must hold plan->workspace_bytes (Stream-K only; may be NULL for Basic).
+ * The Stream-K down is two launches: the split GEMM writing FP32 partial tiles
+ * to `ws`, then the fixup summing them in ascending K order and rounding once. */
 int ffn_mi355x_run(const ffn_mi355x_plan* plan, const void* x, const void* w1,
                    const void* w2, void* hidden, void* out, void* ws, void* hip_stream);
 

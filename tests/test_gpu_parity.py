@@ -159,11 +159,12 @@ def _int_tensor(shape, gen, lo=-2, hi=2):
     return torch.randint(lo, hi + 1, shape, generator=gen).float()
 
 
+@pytest.mark.parametrize("hp", [1024, 128])  # 128: split pieces of one or two K-iterations
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_down_integer_bit_exact_all_variants(dtype):
+def test_down_integer_bit_exact_all_variants(dtype, hp):
     lib = _lib.load()
     gen = torch.Generator().manual_seed(11)
-    mp, hp, np_ = 320, 1024, 448      # ragged against every tile shape
+    mp, np_ = 320, 448                # ragged against every tile shape
     hid = _int_tensor((mp, hp), gen).to(dtype)
     w2 = _int_tensor((np_, hp), gen).to(dtype)
     golden = (hid.double() @ w2.double().T).float().to(dtype)
@@ -178,18 +179,13 @@ def test_down_integer_bit_exact_all_variants(dtype):
                 continue
             say("down-exact", dtype, variant, down, block_num, plan.to_dict())
             out = torch.full((mp, np_), float("nan"), dtype=dtype, device="cuda")
-            ws = torch.zeros(max(1, plan.workspace_bytes // 4), dtype=torch.float32, device="cuda")
+            ws = torch.full((max(1, plan.workspace_bytes // 4),), float("nan"), dtype=torch.float32,
+                            device="cuda")
             _lib.check(lib.ffn_mi355x_down(ctypes.byref(plan), hid_d.data_ptr(), w2_d.data_ptr(),
                                            out.data_ptr(), ws.data_ptr(), stream))
             torch.cuda.synchronize()
             assert torch.equal(out.cpu().view(torch.int16), golden.view(torch.int16)), \
                 (variant, down, block_num)
-            if down == "streamk":  # arrival counters are re-armed to zero on exit
-                partial_bytes = (plan.down_grid * plan.down_slots_per_wg * plan.down_bm
-                                 * plan.down_bn * 4)
-                counters = ws.view(torch.int32)[partial_bytes // 4:
-                                                partial_bytes // 4 + plan.down_sk_tiles]
-                assert int(counters.abs().sum()) == 0
 
 
 def _ordinal(bits16):

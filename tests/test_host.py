@@ -91,8 +91,9 @@ def test_selection():
     assert plan.schedule()["down_sk_tiles"] == 1
     with pytest.raises(NotApplicable):
         make_plan(p, Selection(down_impl="streamk"), 1)
-    with pytest.raises(NotApplicable):   # H spans a single K iteration
-        make_plan(problem_from_shapes([64, 128], [64, 128], [64, 64]), Selection(down_impl="streamk"), 8)
+    with pytest.raises(NotApplicable):   # H spans a single K iteration of a 64-deep tile
+        make_plan(problem_from_shapes([64, 128], [64, 128], [64, 64]), Selection(down_impl="streamk"),
+                  8, down_variant=4)
     for bad in (0, 65536, 8.0, True):
         with pytest.raises(ValueError):
             make_plan(p, Selection(), bad)
@@ -136,8 +137,7 @@ def test_streamk_schedule_exact_once_and_slots(G):
                 for it in range(a, b):
                     seen[it // kI][it % kI] += 1
             assert all(c == 1 for row in seen for c in row)
-            partial = G * n.down_slots_per_wg * n.down_bm * n.down_bn * 4
-            assert n.workspace_bytes >= partial + 4 * sk
+            assert n.workspace_bytes == G * n.down_slots_per_wg * n.down_bm * n.down_bn * 4
 
 
 def test_c_abi_exports_every_declared_symbol():
