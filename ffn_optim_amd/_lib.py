@@ -23,7 +23,7 @@ class PlanStruct(ctypes.Structure):
     """Mirror of ``ffn_mi355x_plan``."""
 
     _fields_ = [(name, ctypes.c_int) for name in (
-        "mp", "kp", "hp", "np", "dtype", "down_impl", "gelu", "block_num",
+        "m", "mp", "kp", "hp", "np", "dtype", "down_impl", "gelu", "block_num",
         "up_variant", "down_variant", "up_bm", "up_bn", "up_bk",
         "down_bm", "down_bn", "down_bk", "up_tiles", "up_grid",
         "down_tiles", "down_grid", "down_k_iters", "down_dp_tiles",
@@ -38,7 +38,7 @@ _vp = ctypes.c_void_p
 _i = ctypes.c_int
 SIGNATURES = {
     "ffn_mi355x_query": (_i, [_i, _P(_i), ctypes.c_char_p, _i]),
-    "ffn_mi355x_make_plan": (_i, [_i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _P(PlanStruct)]),
+    "ffn_mi355x_make_plan": (_i, [_i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _P(PlanStruct)]),
     "ffn_mi355x_workspace_bytes": (_i, [_P(PlanStruct), _P(ctypes.c_size_t)]),
     "ffn_mi355x_run": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ffn_mi355x_up": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp]),
@@ -98,9 +98,11 @@ def query(device: int) -> tuple[int, str]:
 
 
 def make_plan(mp, kp, hp, np_, dtype, down_impl, gelu, block_num, up_variant=-1,
-              down_variant=-1) -> PlanStruct:
+              down_variant=-1, m=None) -> PlanStruct:
+    """Native plan; `m` is the logical row count (default: all mp rows hold data)."""
     plan = PlanStruct()
-    check(load().ffn_mi355x_make_plan(mp, kp, hp, np_, dtype, DOWN_CODES[down_impl],
+    check(load().ffn_mi355x_make_plan(mp if m is None else m, mp, kp, hp, np_, dtype,
+                                      DOWN_CODES[down_impl],
                                       GELU_CODES[gelu], block_num, up_variant, down_variant,
                                       ctypes.byref(plan)))
     return plan

@@ -11,8 +11,9 @@
 // Data path of one macro tile (BM x BN, reduction step BK):
 //   HBM/L2 --buffer_load_dwordx4 ... lds--> LDS stage s  (no VGPR staging)
 //   LDS --ds_read_b128--> A/B fragments --v_mfma_f32_32x32x16_{bf16,f16}--> FP32 acc
-// LDS rows are BK*2 bytes; the 16-byte chunk c of row r lives at c ^ swz(r) so
-// that the 8 lanes served per LDS cycle hit 8 distinct bank groups.  Out-of-range
+// LDS rows are BK*2 bytes; the 16-byte chunk c of row r lives at c ^ ((r / R256) mod CH),
+// R256 = rows per 256-byte line of the 64 LDS banks: the 16 lanes of one ds_read_b128 cycle
+// (16 consecutive rows, one chunk) then cover all 64 banks exactly once.  Out-of-range
 // rows and the K tail read as zero through the buffer descriptor's range check,
 // so tiles may overhang the matrices and no load can leave its buffer.
 //
@@ -43,6 +44,7 @@ struct GemmParams {
     void* c;              // [M][ldc]   hidden or out
     float* ws;            // Stream-K partial-tile slots (FP32)
     int M, N, K;
+    int m_valid;          // rows of A holding data; rows [m_valid, M) are zero padding
     int lda, ldb, ldc;
     int tiles_m, tiles_n;
     int k_iters;          // ceil(K / BK)
@@ -53,10 +55,14 @@ struct GemmParams {
     int group_m;          // tile-order swizzle: tiles walk group_m tile-rows column by column
 };
 
-template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int STAGES_>
+// SYNCQ_: MFMA slot of a stage's last k-step after which the stage wait + barrier is placed
+// (-1: end of the first block of B).  DMAKS_: k-steps of an iteration carrying the refill DMA
+// with two stages (-1: the first half).
+template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int STAGES_, int SYNCQ_ = -1, int DMAKS_ = -1>
 struct TileCfg {
     static constexpr int BM = BM_, BN = BN_, BK = BK_;
     static constexpr int WGM = WGM_, WGN = WGN_, STAGES = STAGES_;
+    static constexpr int SYNCQ = SYNCQ_, DMAKS = DMAKS_;
     static constexpr int NW = WGM * WGN;           // waves per workgroup
     static constexpr int NT = NW * 64;             // threads per workgroup
     static constexpr int WTM = BM / WGM, WTN = BN / WGN;  // wave tile
@@ -64,7 +70,10 @@ struct TileCfg {
     static constexpr int ROWB = BK * 2;            // bytes of one LDS row
     static constexpr int CH = ROWB / 16;           // 16-byte chunks per row
     static constexpr int RPB = 1024 / ROWB;        // rows per 1 KiB DMA block (64 lanes x 16 B)
-    static constexpr int RPL = (ROWB >= 128) ? 1 : 128 / ROWB;  // rows per 128-byte bank line
+    static constexpr int R256 = (ROWB >= 256) ? 1 : 256 / ROWB; // rows per 256-byte bank line
+    // The swizzle of a row depends on (row / R256) mod CH; seen from a 1 KiB DMA block it
+    // repeats every SWZ_PERIOD blocks.
+    static constexpr int SWZ_PERIOD = (CH * R256 > RPB) ? (CH * R256) / RPB : 1;
     static constexpr int A_BYTES = BM * ROWB, B_BYTES = BN * ROWB;
     static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
     static constexpr int A_BLKS = A_BYTES / 1024, B_BLKS = B_BYTES / 1024;
@@ -75,7 +84,10 @@ struct TileCfg {
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
     static_assert(ROWB % 16 == 0 && CH >= 2, "BK must be a multiple of 16");
     static_assert(A_BLKS % NW == 0 && B_BLKS % NW == 0, "DMA blocks must split evenly over waves");
-    static_assert(32 % (CH * RPL) == 0 || (CH * RPL) % 32 == 0, "swizzle period");
+    static_assert(32 % (CH * R256) == 0, "fragment rows start on a swizzle period");
+    static_assert(SWZ_PERIOD <= 2, "at most two DMA offset sets");
+    static_assert(SWZ_PERIOD == 1 || (A_PW % 2 == 0 && B_PW % 2 == 0),
+                  "block parity of every DMA instruction must be known at compile time");
     static_assert(LDS_BYTES <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
 };
 
@@ -273,8 +285,7 @@ struct Engine {
     int tid, lane, wave, wm, wn;
     int a_row_off, b_row_off;  // per-lane LDS byte offsets of the fragment rows
     int swz;                   // chunk XOR of this lane's fragment rows
-    int dma_a, dma_b;          // per-lane DMA source offsets inside a block (without k0)
-    int dma_k;                 // K element of this lane's DMA chunk (without k0)
+    static __device__ __forceinline__ int swz_of(int row) { return (row / C::R256) % C::CH; }
 
     __device__ __forceinline__ Engine(lds_char* s, const GemmParams& p) : smem(s) {
         tid = threadIdx.x;
@@ -285,13 +296,7 @@ struct Engine {
         const int r = lane & 31;
         a_row_off = (wm * C::WTM + r) * C::ROWB;
         b_row_off = C::A_BYTES + (wn * C::WTN + r) * C::ROWB;
-        swz = (r / C::RPL) % C::CH;
-        // DMA: this lane fills physical chunk (lane % CH) of row (lane / CH) of each 1 KiB block,
-        // i.e. logical chunk pc ^ swz(row); the swizzle depends only on the row inside the block.
-        const int rl = lane / C::CH, pc = lane % C::CH;
-        dma_k = (pc ^ ((rl / C::RPL) % C::CH)) * 8;
-        dma_a = rl * p.lda * 2 + dma_k * 2;
-        dma_b = rl * p.ldb * 2 + dma_k * 2;
+        swz = swz_of(r);
     }
 
     __device__ __forceinline__ void rsrc(const GemmParams& p, const Unit& u,
@@ -300,48 +305,65 @@ struct Engine {
         const int lda2 = p.lda * 2, ldb2 = p.ldb * 2;
         const char* abase = (const char*)p.a + (size_t)row0 * (size_t)lda2;
         const char* bbase = (const char*)p.b + (size_t)col0 * (size_t)ldb2;
-        ra = make_rsrc(abase, (uint32_t)min(C::BM, p.M - row0) * (uint32_t)lda2);
+        // zero-padding rows of A are not fetched: past m_valid the range check returns zeros
+        ra = make_rsrc(abase, (uint32_t)max(0, min(C::BM, p.m_valid - row0)) * (uint32_t)lda2);
         rb = make_rsrc(bbase, (uint32_t)min(C::BN, p.N - col0) * (uint32_t)ldb2);
     }
 
-    // DMA source offsets of this lane for K-iteration `kit`.  Chunks past K get an offset
-    // >= 2^31, beyond any range, and read as zero (rows past the operand are out of range of
-    // the tile's descriptor).  The whole offset travels in the VGPR operand: the buffer range
-    // check covers voffset but not soffset.
-    __device__ __forceinline__ void dma_offsets(const GemmParams& p, int kit, uint32_t& va,
-                                                uint32_t& vb) const {
+    // DMA source offsets of this lane for K-iteration `kit` (even and odd blocks).  Chunks past
+    // K get an offset >= 2^31, beyond any range, and read as zero (rows past the operand are
+    // out of range of the tile's descriptor).  The whole offset travels in the VGPR operand:
+    // the buffer range check covers voffset but not soffset.
+    struct DmaOff {
+        uint32_t a[2], b[2];
+    };
+    __device__ __forceinline__ DmaOff dma_offsets(const GemmParams& p, int kit) const {
+        // recomputed from an opaque lane id at every use: held across the persistent loop these
+        // per-lane constants get spilled, and each reload drains the outstanding DMA
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int rl = ln / C::CH, pc = ln % C::CH;
+        DmaOff o;
         const int k0 = kit * C::BK;
-        const bool ok = (k0 + C::BK <= p.K) || (k0 + dma_k < p.K);
-        va = ok ? (uint32_t)(dma_a + k0 * 2) : 0x80000000u;
-        vb = ok ? (uint32_t)(dma_b + k0 * 2) : 0x80000000u;
+#pragma unroll
+        for (int par = 0; par < C::SWZ_PERIOD; ++par) {
+            // this lane fills physical chunk pc of row rl of each 1 KiB block, i.e. logical chunk
+            // pc ^ swz(row); the swizzle of a block's rows depends only on the block's parity
+            const int kk = (pc ^ swz_of(par * C::RPB + rl)) * 8;
+            const bool ok = (k0 + C::BK <= p.K) || (k0 + kk < p.K);
+            o.a[par] = ok ? (uint32_t)(rl * p.lda * 2 + (k0 + kk) * 2) : 0x80000000u;
+            o.b[par] = ok ? (uint32_t)(rl * p.ldb * 2 + (k0 + kk) * 2) : 0x80000000u;
+        }
+        if constexpr (C::SWZ_PERIOD == 1) o.a[1] = o.a[0], o.b[1] = o.b[0];
+        return o;
     }
 
     // DMA instruction D (of the LOADS this wave issues per stage) into LDS stage `stage`.
     template <int D>
     __device__ __forceinline__ void issue_one(const GemmParams& p, const __amdgpu_buffer_rsrc_t& ra,
                                               const __amdgpu_buffer_rsrc_t& rb, int stage,
-                                              uint32_t va, uint32_t vb) const {
+                                              const DmaOff& o) const {
         lds_char* st = smem + stage * C::STAGE_BYTES;
         if constexpr (D < C::A_PW) {
             const int blk = wave * C::A_PW + D;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 ra, (__attribute__((address_space(3))) void*)(st + blk * 1024), 16,
-                (int)(va + (uint32_t)blk * (uint32_t)(C::RPB * p.lda * 2)), 0, 0, 0);
+                (int)(o.a[D & 1] + (uint32_t)blk * (uint32_t)(C::RPB * p.lda * 2)), 0, 0, 0);
         } else {
             const int blk = wave * C::B_PW + (D - C::A_PW);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rb, (__attribute__((address_space(3))) void*)(st + C::A_BYTES + blk * 1024), 16,
-                (int)(vb + (uint32_t)blk * (uint32_t)(C::RPB * p.ldb * 2)), 0, 0, 0);
+                (int)(o.b[(D - C::A_PW) & 1] + (uint32_t)blk * (uint32_t)(C::RPB * p.ldb * 2)), 0, 0, 0);
         }
     }
 
     template <int D0, int D1>
     __device__ __forceinline__ void issue_range(const GemmParams& p, const __amdgpu_buffer_rsrc_t& ra,
                                                 const __amdgpu_buffer_rsrc_t& rb, int stage,
-                                                uint32_t va, uint32_t vb) const {
+                                                const DmaOff& o) const {
         if constexpr (D0 < D1) {
-            issue_one<D0>(p, ra, rb, stage, va, vb);
-            issue_range<D0 + 1, D1>(p, ra, rb, stage, va, vb);
+            issue_one<D0>(p, ra, rb, stage, o);
+            issue_range<D0 + 1, D1>(p, ra, rb, stage, o);
         }
     }
 
@@ -352,11 +374,7 @@ struct Engine {
         rsrc(p, u, ra, rb);
 #pragma unroll
         for (int s = 0; s < S - 1; ++s)
-            if (u.kb + s < u.ke) {
-                uint32_t va, vb;
-                dma_offsets(p, u.kb + s, va, vb);
-                issue_range<0, C::LOADS>(p, ra, rb, s, va, vb);
-            }
+            if (u.kb + s < u.ke) issue_range<0, C::LOADS>(p, ra, rb, s, dma_offsets(p, u.kb + s));
     }
 
     // Fragment registers: A (activation rows) double-buffered across k-steps, B (weight rows)
@@ -406,17 +424,19 @@ struct Engine {
     static constexpr int NM = FN * FM;
     // slot of the last k-step after whose MFMA the stage wait + barrier is placed: the end of
     // the j = 0 block, from where every B fragment can be reloaded after its last use
-    static constexpr int SYNC_Q = FM - 1;
+    static constexpr int SYNC_Q = C::SYNCQ >= 0 ? C::SYNCQ : FM - 1;
+    static_assert(SYNC_Q >= FM - 1 && SYNC_Q < NM, "the barrier may not precede the in-place B reloads");
     // Slots carrying the refill DMA.  With two stages the data is waited for at the end of the
     // same iteration, so it goes out in the first half; with more, it is spread over every slot
     // before the stage wait (whose count assumes whole groups issued).
-    static constexpr int DMA_SLOTS = (S == 2) ? (KS / 2) * NM : (KS - 1) * NM + SYNC_Q;
+    static constexpr int DMA_SLOTS = (S == 2) ? (C::DMAKS > 0 ? C::DMAKS : KS / 2) * NM
+                                              : (KS - 1) * NM + SYNC_Q;
     static_assert(KS >= 2 && DMA_SLOTS >= 1, "at least two k-steps per stage");
 
     template <int CB, int MODE, bool DMA, int KSI, int Q>
     __device__ __forceinline__ void slot(const GemmParams& p, f32x16 (&acc)[FN][FM], int cur, int nxt,
                                          const __amdgpu_buffer_rsrc_t& ra, const __amdgpu_buffer_rsrc_t& rb,
-                                         int dma_stage, uint32_t va, uint32_t vb, const Unit& nx) {
+                                         int dma_stage, const DmaOff& o, const Unit& nx) {
         constexpr int j = Q / FM, i = Q % FM;
         acc[j][i] = mfma32<DT>(fb[j], fa[CB][i], acc[j][i]);
         constexpr int NB = 1 - CB;
@@ -449,7 +469,7 @@ struct Engine {
         constexpr int g = KSI * NM + Q;  // this slot's share of the refill DMA
         if constexpr (DMA && g < DMA_SLOTS && (KSI + 1 < KS || Q < SYNC_Q)) {
             constexpr int t0 = g * C::LOADS / DMA_SLOTS, t1 = (g + 1) * C::LOADS / DMA_SLOTS;
-            issue_range<t0, t1>(p, ra, rb, dma_stage, va, vb);
+            issue_range<t0, t1>(p, ra, rb, dma_stage, o);
         }
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -457,10 +477,10 @@ struct Engine {
     template <int CB, int MODE, bool DMA, int KSI, int Q>
     __device__ __forceinline__ void slots(const GemmParams& p, f32x16 (&acc)[FN][FM], int cur, int nxt,
                                           const __amdgpu_buffer_rsrc_t& ra, const __amdgpu_buffer_rsrc_t& rb,
-                                          int dma_stage, uint32_t va, uint32_t vb, const Unit& nx) {
+                                          int dma_stage, const DmaOff& o, const Unit& nx) {
         if constexpr (Q < NM) {
-            slot<CB, MODE, DMA, KSI, Q>(p, acc, cur, nxt, ra, rb, dma_stage, va, vb, nx);
-            slots<CB, MODE, DMA, KSI, Q + 1>(p, acc, cur, nxt, ra, rb, dma_stage, va, vb, nx);
+            slot<CB, MODE, DMA, KSI, Q>(p, acc, cur, nxt, ra, rb, dma_stage, o, nx);
+            slots<CB, MODE, DMA, KSI, Q + 1>(p, acc, cur, nxt, ra, rb, dma_stage, o, nx);
         }
     }
 
@@ -468,14 +488,14 @@ struct Engine {
     __device__ __forceinline__ void ksteps(const GemmParams& p, const Unit& nx,
                                            const __amdgpu_buffer_rsrc_t& ra,
                                            const __amdgpu_buffer_rsrc_t& rb, int cur, int dstage,
-                                           uint32_t va, uint32_t vb, f32x16 (&acc)[FN][FM]) {
+                                           const DmaOff& o, f32x16 (&acc)[FN][FM]) {
         if constexpr (KSI < KS) {
             constexpr int MODE = (KSI + 1 < KS) ? 0 : (LAST ? 2 : 1);
             const int nxt = (cur + 1 == S) ? 0 : cur + 1;
             // the last iteration of a unit refills nothing (its DMA prologue for the next unit
             // is issued after the barrier of its last k-step)
-            slots<KSI & 1, MODE, !LAST, KSI, 0>(p, acc, cur, nxt, ra, rb, dstage, va, vb, nx);
-            ksteps<LAST, KSI + 1>(p, nx, ra, rb, cur, dstage, va, vb, acc);
+            slots<KSI & 1, MODE, !LAST, KSI, 0>(p, acc, cur, nxt, ra, rb, dstage, o, nx);
+            ksteps<LAST, KSI + 1>(p, nx, ra, rb, cur, dstage, o, acc);
         }
     }
 
@@ -503,13 +523,12 @@ struct Engine {
         for (int it = 0; it < n - 1; ++it) {
             const int dkit = it + S - 1;
             const bool real = dkit < n;
-            uint32_t va, vb;
-            dma_offsets(p, u.kb + dkit, va, vb);
+            const DmaOff o = dma_offsets(p, u.kb + dkit);
             const int dstage = (cur == 0) ? S - 1 : cur - 1;
-            ksteps<false, 0>(p, nx, real ? ra : rnull, real ? rb : rnull, cur, dstage, va, vb, acc);
+            ksteps<false, 0>(p, nx, real ? ra : rnull, real ? rb : rnull, cur, dstage, o, acc);
             cur = (cur + 1 == S) ? 0 : cur + 1;
         }
-        ksteps<true, 0>(p, nx, ra, rb, cur, 0, 0u, 0u, acc);
+        ksteps<true, 0>(p, nx, ra, rb, cur, 0, DmaOff{}, acc);
     }
 
     // Output position of accumulator group (j, i, q): row m, columns n..n+3.
@@ -548,6 +567,71 @@ struct Engine {
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
+    }
+
+    // ---- epilogue through LDS --------------------------------------------------------------
+    // The accumulators of a lane cover 4 consecutive columns of 16 different rows, so storing
+    // them directly writes every 128-byte output line in eight 16-byte pieces spread over time,
+    // which the memory side pays for dearly.  Instead the tile is activated and cast in
+    // registers, written into LDS stage S-1 (the one the next unit's DMA prologue does not
+    // fill) in chunks of ER rows, and copied out with full-row 16-byte-per-lane stores.
+    static constexpr int OUT_STRIDE = C::BN * 2 + 16;  // LDS bytes per staged output row
+    static constexpr int ER_FIT = C::STAGE_BYTES / OUT_STRIDE;
+    static constexpr int ER = ER_FIT >= C::BM ? C::BM : (ER_FIT >= 128 ? 128 : (ER_FIT >= 64 ? 64 : 32));
+    static_assert(ER * OUT_STRIDE <= C::STAGE_BYTES && ER % 32 == 0 && C::BM % ER == 0,
+                  "an output chunk fits one LDS stage");
+    static constexpr int TPR = C::BN / 8;                // 16-byte pieces per output row
+    static constexpr int PIECES = ER * TPR / NT;         // pieces per thread per chunk
+    static_assert((ER * TPR) % NT == 0, "chunk pieces split evenly over the threads");
+
+    template <int EPI>
+    __device__ __forceinline__ void store_tile_lds(const GemmParams& p, const Unit& u, bool next,
+                                                   f32x16 (&acc)[FN][FM]) {
+        lds_char* eb = smem + (S - 1) * C::STAGE_BYTES;
+        // DMA still in flight may target any stage but the next unit's prologue (issued last):
+        // drain it, then make sure every wave has, before the staging area is written
+        if (next) wait_vmcnt<C::LOADS * (S - 1)>();
+        else wait_vmcnt<0>();
+        const int row0 = u.tm * C::BM, col0 = u.tn * C::BN;
+        // opaque copies: the addressing below depends only on the thread id, and would
+        // otherwise be hoisted out of the persistent loop and held (spilled) across it
+        int ln = lane, td = tid;
+        asm volatile("" : "+v"(ln));
+        asm volatile("" : "+v"(td));
+#pragma unroll
+        for (int c = 0; c < C::BM / ER; ++c) {
+            barrier();
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                const int rt = wm * C::WTM + 32 * i;  // first tile row of block i (wave-uniform)
+                if (rt / ER != c) continue;
+                const int rl = rt - c * ER + (ln & 31);
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int nt = wn * C::WTN + 32 * j + 8 * q + 4 * (ln >> 5);
+                        const uint2 v = pack4<DT>(activate<EPI>(acc[j][i][4 * q]),
+                                                  activate<EPI>(acc[j][i][4 * q + 1]),
+                                                  activate<EPI>(acc[j][i][4 * q + 2]),
+                                                  activate<EPI>(acc[j][i][4 * q + 3]));
+                        *(__attribute__((address_space(3))) unsigned long long*)(eb + rl * OUT_STRIDE + nt * 2) =
+                            __builtin_bit_cast(unsigned long long, v);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            barrier();
+#pragma unroll
+            for (int k = 0; k < PIECES; ++k) {
+                const int idx = k * NT + td;
+                const int r = idx / TPR, ch = idx - r * TPR;
+                const u32x4 v = *(const __attribute__((address_space(3))) u32x4*)(eb + r * OUT_STRIDE + ch * 16);
+                const int gm = row0 + c * ER + r, gn = col0 + ch * 8;
+                if (gm < p.M && gn < p.N)
+                    *(u32x4*)((char*)p.c + ((size_t)gm * (size_t)p.ldc + (size_t)gn) * 2) = v;
+            }
+        }
     }
 
     // FP32 partial tile in the accumulator's own register order: group (j, i, q) of thread
@@ -593,7 +677,7 @@ __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
         if (SK && u.split >= 0)
             eng.store_partial(sk_slot(p, v, u.local, C::BM * C::BN), acc);
         else
-            eng.template store_tile<EPI>(p, u.tm, u.tn, acc);
+            eng.template store_tile_lds<EPI>(p, u, nx.valid, acc);
         if (!nx.valid) break;
         u = nx;
     }

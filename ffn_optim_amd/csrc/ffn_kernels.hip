@@ -12,10 +12,10 @@
 namespace {
 template <int ID>
 struct VariantCfg;
-#define FFN_DEFINE_CFG(id, bm, bn, bk, wgm, wgn, st) \
-    template <>                                       \
-    struct VariantCfg<id> {                           \
-        using type = ffn::TileCfg<bm, bn, bk, wgm, wgn, st>; \
+#define FFN_DEFINE_CFG(id, bm, bn, bk, wgm, wgn, st, ...)           \
+    template <>                                                     \
+    struct VariantCfg<id> {                                         \
+        using type = ffn::TileCfg<bm, bn, bk, wgm, wgn, st, ##__VA_ARGS__>; \
     };
 FFN_VARIANTS(FFN_DEFINE_CFG)
 #undef FFN_DEFINE_CFG

@@ -14,6 +14,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
 #include <string>
 
 #include "ffn_gemm.hpp"
@@ -26,7 +27,7 @@
 
 typedef hipError_t (*ffn_launch_fn)(int role, const ffn::GemmParams* p, int grid, hipStream_t stream);
 
-#define FFN_DECLARE_LAUNCHERS(id, bm, bn, bk, wgm, wgn, st)                                      \
+#define FFN_DECLARE_LAUNCHERS(id, bm, bn, bk, wgm, wgn, st, ...)                                    \
     extern "C" hipError_t ffn_launch_d0_v##id(int, const ffn::GemmParams*, int, hipStream_t); \
     extern "C" hipError_t ffn_launch_d1_v##id(int, const ffn::GemmParams*, int, hipStream_t);
 FFN_VARIANTS(FFN_DECLARE_LAUNCHERS)
@@ -41,7 +42,7 @@ struct Variant {
     int lds() const { return stages * (bm + bn) * bk * 2; }
 };
 
-#define FFN_VARIANT_ROW(id, bm, bn, bk, wgm, wgn, st) \
+#define FFN_VARIANT_ROW(id, bm, bn, bk, wgm, wgn, st, ...) \
     {bm, bn, bk, wgm, wgn, st, {ffn_launch_d0_v##id, ffn_launch_d1_v##id}},
 const Variant kVariants[] = {FFN_VARIANTS(FFN_VARIANT_ROW)};
 #undef FFN_VARIANT_ROW
@@ -67,18 +68,47 @@ int ok() {
 
 long long cdiv(long long a, long long b) { return (a + b - 1) / b; }
 
-// Relative MFMA efficiency of a macro tile.  A tile's work per byte staged through LDS and
-// L2 grows with BM*BN/(BM+BN); 256x256 is the reference point.
+// ---- planning -------------------------------------------------------------------------
+// A small time model picks the tile: per-workgroup time = work units x per-iteration time,
+// where an iteration is bounded by the tile's MFMA rate and by the loads the workgroup can
+// keep in flight ((S-1) stages over the memory latency), and the whole GEMM by streaming
+// its operands from HBM once.  Rates are measured on MI355X (sustained clock ~1.8-2 GHz).
+constexpr double kCuMfmaRate = 4.5e12;     // FLOP/s per CU a 256x256 tile sustains
+constexpr double kCuLoadRate = 60e9;       // B/s per CU of LDS-DMA alongside MFMA work
+constexpr double kLoadLatency = 1.5e-6;    // s, HBM-miss load latency under load
+constexpr double kHbmRate = 6.5e12;        // B/s sustained HBM read rate
+constexpr double kLaunch = 3e-6;           // s, one extra kernel launch (Stream-K fixup)
+constexpr double kReduceRate = 3.0e12;     // B/s of the fixup kernel
+
+// Relative MFMA efficiency of each macro tile (measured, 256x256 = 1).
 double tile_eff(const Variant& v) {
     const double intensity = (double)v.bm * v.bn / (double)(v.bm + v.bn);
-    return intensity >= 128.0 ? 1.0 : intensity / 128.0;
+    double e = intensity >= 128.0 ? 1.0 : intensity / 128.0;
+    if (v.bm == 256 && v.bn == 128) e = 0.97;
+    if (v.bm == 128 && v.bn == 256) e = 0.97;
+    if (v.bm == 128 && v.bn == 128) e = 0.63;
+    return e;
 }
 
-// Estimated time (arbitrary units) of a data-parallel GEMM over [M x N] with K depth.
-double cost_basic(const Variant& v, long long M, long long N, long long K, int G) {
+// Seconds per BK-deep iteration of one workgroup on a tile with `rows` data-bearing rows.
+double iter_time(const Variant& v, long long rows) {
+    const double flops = 2.0 * v.bm * v.bn * v.bk;
+    const double t_mfma = flops / (kCuMfmaRate * tile_eff(v));
+    const double bytes = (double)(rows + v.bn) * v.bk * 2.0;
+    const double inflight = (double)(v.stages - 1) * (double)(v.bm + v.bn) * v.bk * 2.0;
+    const double rate = std::min(kCuLoadRate, inflight / kLoadLatency);
+    return std::max(t_mfma, bytes / rate);
+}
+
+long long rows_in_tile(const Variant& v, long long m_valid) { return std::min<long long>(v.bm, m_valid); }
+
+// Estimated seconds of a data-parallel GEMM [M x N] (m_valid data rows), depth K.
+double cost_basic(const Variant& v, long long M, long long m_valid, long long N, long long K, int G) {
     const long long T = cdiv(M, v.bm) * cdiv(N, v.bn);
     const long long waves = cdiv(T, G);
-    return (double)waves * v.bm * v.bn * (double)(cdiv(K, v.bk) * v.bk) / tile_eff(v);
+    const double t = (double)waves * (double)cdiv(K, v.bk) * iter_time(v, rows_in_tile(v, m_valid));
+    const double hbm = (double)(N * K + m_valid * K) * 2.0 / kHbmRate;
+    return std::max(t, hbm);
 }
 
 struct SkShape {
@@ -99,33 +129,41 @@ bool sk_shape(const Variant& v, long long M, long long N, long long K, int G, Sk
     return s.sk > 0 && s.k_iters >= 2;
 }
 
-double cost_streamk(const Variant& v, const SkShape& s, int G) {
-    const double it = (double)v.bm * v.bn * v.bk / tile_eff(v);
+double cost_streamk(const Variant& v, const SkShape& s, long long m_valid, long long N, long long K,
+                    int G) {
+    const double it = iter_time(v, rows_in_tile(v, m_valid));
     const long long dp_waves = cdiv(s.dp, G);
     const long long sk_iters = s.q + (s.r ? 1 : 0);
-    // publishing and re-reading an FP32 partial costs about two K-iterations of the tile
-    const double fixup = (s.k_iters > sk_iters) ? 2.0 : 0.0;
-    return it * ((double)dp_waves * s.k_iters + (double)sk_iters + fixup);
+    double t = it * ((double)dp_waves * s.k_iters + (double)sk_iters);
+    // shared split tiles: FP32 partials written, re-read and reduced by a second launch
+    const long long pieces_per_tile = std::min<long long>(G, cdiv(s.k_iters, std::max<long long>(1, s.q)) + 1);
+    if (s.k_iters > sk_iters) {
+        const double tile_bytes = (double)v.bm * v.bn * 4.0;
+        t += kLaunch + (double)s.sk * (double)pieces_per_tile * 2.0 * tile_bytes / kReduceRate +
+             tile_bytes / kCuLoadRate;
+    }
+    const double hbm = (double)(N * K + m_valid * K) * 2.0 / kHbmRate;
+    return std::max(t, hbm);
 }
 
-int pick_basic(long long M, long long N, long long K, int G) {
+int pick_basic(long long M, long long m_valid, long long N, long long K, int G) {
     int best = 0;
     double best_cost = 1e300;
     for (int i = 0; i < kNumVariants; ++i) {
-        const double c = cost_basic(kVariants[i], M, N, K, G);
-        if (c < best_cost) best_cost = c, best = i;
+        const double c = cost_basic(kVariants[i], M, m_valid, N, K, G);
+        if (c < best_cost * 0.999) best_cost = c, best = i;
     }
     return best;
 }
 
-int pick_streamk(long long M, long long N, long long K, int G) {
+int pick_streamk(long long M, long long m_valid, long long N, long long K, int G) {
     int best = -1;
     double best_cost = 1e300;
     for (int i = 0; i < kNumVariants; ++i) {
         SkShape s;
         if (!sk_shape(kVariants[i], M, N, K, G, s)) continue;
-        const double c = cost_streamk(kVariants[i], s, G);
-        if (c < best_cost) best_cost = c, best = i;
+        const double c = cost_streamk(kVariants[i], s, m_valid, N, K, G);
+        if (c < best_cost * 0.999) best_cost = c, best = i;
     }
     return best;
 }
@@ -133,7 +171,7 @@ int pick_streamk(long long M, long long N, long long K, int G) {
 int group_m_for(long long tiles_m) { return (int)(tiles_m < 8 ? tiles_m : 8); }
 
 bool valid_plan(const ffn_mi355x_plan* p) {
-    return p && p->up_variant >= 0 && p->up_variant < kNumVariants && p->down_variant >= 0 &&
+    return p && p->m >= 1 && p->m <= p->mp && p->up_variant >= 0 && p->up_variant < kNumVariants && p->down_variant >= 0 &&
            p->down_variant < kNumVariants && (p->dtype == 0 || p->dtype == 1) &&
            (p->down_impl == FFN_MI355X_DOWN_BASIC || p->down_impl == FFN_MI355X_DOWN_STREAMK) &&
            (p->gelu == 0 || p->gelu == 1) && p->block_num >= 1;
@@ -167,9 +205,11 @@ int ffn_mi355x_query(int device, int* cu_count, char* arch, int arch_len) {
     return ok();
 }
 
-int ffn_mi355x_make_plan(int mp, int kp, int hp, int np, int dtype, int down_impl, int gelu,
+int ffn_mi355x_make_plan(int m, int mp, int kp, int hp, int np, int dtype, int down_impl, int gelu,
                          int block_num, int up_variant, int down_variant, ffn_mi355x_plan* plan) {
     if (!plan) return fail(FFN_MI355X_EINVAL, "plan must not be NULL");
+    if (m <= 0 || m > mp)
+        return fail(FFN_MI355X_EINVAL, "logical rows m must be in [1, mp] (got m=%d mp=%d)", m, mp);
     if (dtype != FFN_MI355X_FP16 && dtype != FFN_MI355X_BF16)
         return fail(FFN_MI355X_EINVAL, "dtype must be float16 or bfloat16");
     if (gelu != FFN_MI355X_GELU_ERF && gelu != FFN_MI355X_GELU_RATIONAL)
@@ -192,12 +232,13 @@ int ffn_mi355x_make_plan(int mp, int kp, int hp, int np, int dtype, int down_imp
         return fail(FFN_MI355X_EINVAL, "tile variant out of range (0..%d)", kNumVariants - 1);
 
     memset(plan, 0, sizeof *plan);
+    plan->m = m;
     plan->mp = mp, plan->kp = kp, plan->hp = hp, plan->np = np;
     plan->dtype = dtype, plan->down_impl = down_impl, plan->gelu = gelu, plan->block_num = block_num;
     const int G = block_num;
 
     // up: [mp x hp], depth kp
-    const int uv = up_variant >= 0 ? up_variant : pick_basic(mp, hp, kp, G);
+    const int uv = up_variant >= 0 ? up_variant : pick_basic(mp, m, hp, kp, G);
     const Variant& U = kVariants[uv];
     plan->up_variant = uv;
     plan->up_bm = U.bm, plan->up_bn = U.bn, plan->up_bk = U.bk;
@@ -218,7 +259,7 @@ int ffn_mi355x_make_plan(int mp, int kp, int hp, int np, int dtype, int down_imp
             }
             dv = down_variant;
         } else {
-            dv = pick_streamk(mp, np, hp, G);
+            dv = pick_streamk(mp, m, np, hp, G);
             if (dv < 0) {
                 bool any_two = false;
                 for (int i = 0; i < kNumVariants; ++i) any_two |= cdiv(hp, kVariants[i].bk) >= 2;
@@ -230,7 +271,7 @@ int ffn_mi355x_make_plan(int mp, int kp, int hp, int np, int dtype, int down_imp
             }
         }
     } else {
-        dv = down_variant >= 0 ? down_variant : pick_basic(mp, np, hp, G);
+        dv = down_variant >= 0 ? down_variant : pick_basic(mp, m, np, hp, G);
     }
     const Variant& D = kVariants[dv];
     plan->down_variant = dv;
@@ -268,6 +309,7 @@ int ffn_mi355x_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, vo
     memset(&gp, 0, sizeof gp);
     gp.a = x, gp.b = w1, gp.c = hidden;
     gp.M = plan->mp, gp.N = plan->hp, gp.K = plan->kp;
+    gp.m_valid = plan->m;
     gp.lda = plan->kp, gp.ldb = plan->kp, gp.ldc = plan->hp;
     gp.tiles_m = (int)cdiv(plan->mp, U.bm), gp.tiles_n = (int)cdiv(plan->hp, U.bn);
     gp.k_iters = (int)cdiv(plan->kp, U.bk);
@@ -286,6 +328,7 @@ int ffn_mi355x_down(const ffn_mi355x_plan* plan, const void* hidden, const void*
     memset(&gp, 0, sizeof gp);
     gp.a = hidden, gp.b = w2, gp.c = out;
     gp.M = plan->mp, gp.N = plan->np, gp.K = plan->hp;
+    gp.m_valid = plan->m;
     gp.lda = plan->hp, gp.ldb = plan->hp, gp.ldc = plan->np;
     gp.tiles_m = (int)cdiv(plan->mp, D.bm), gp.tiles_n = (int)cdiv(plan->np, D.bn);
     gp.k_iters = plan->down_k_iters;

@@ -1,6 +1,8 @@
 // ffn_variants.hpp -- the macro-tile variants compiled into libffn_mi355x.so.
 //
-// X(id, BM, BN, BK, waves along M, waves along N, LDS stages)
+// X(id, BM, BN, BK, waves along M, waves along N, LDS stages[, sync slot, DMA k-steps])
+// The deep-pipeline 64-row tiles (8, 9) keep 100+ KiB of loads in flight per CU for the
+// memory-bound small-M (decode) shapes.
 // Each variant is built for both storage types and four epilogues (GELU-erf,
 // GELU-rational, plain store, plain store + Stream-K split) in its own object.
 #pragma once
@@ -12,9 +14,12 @@
     X(3, 128, 128, 64, 2, 2, 2)         \
     X(4, 64, 64, 64, 2, 2, 2)           \
     X(5, 64, 128, 64, 2, 2, 3)          \
-    X(6, 256, 256, 32, 2, 2, 4)
+    X(6, 256, 256, 32, 2, 2, 4)         \
+    X(7, 256, 256, 32, 2, 2, 5)         \
+    X(8, 64, 64, 64, 2, 2, 8)           \
+    X(9, 64, 128, 64, 2, 2, 6)
 
-#define FFN_NUM_VARIANTS 7
+#define FFN_NUM_VARIANTS 10
 
 // launch roles of one variant
 enum { FFN_ROLE_UP_ERF = 0, FFN_ROLE_UP_RATIONAL = 1, FFN_ROLE_DOWN_BASIC = 2, FFN_ROLE_DOWN_STREAMK = 3 };

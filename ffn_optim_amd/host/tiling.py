@@ -103,7 +103,7 @@ def make_plan(problem, selection=Selection(), block_num=DEFAULT_BLOCK_NUM, *, ge
     dtype = _lib.BF16 if problem.dtype == "bfloat16" else _lib.FP16
     native = _lib.make_plan(mp, kp, hp, np_, dtype, selection.down_impl, gelu, block_num,
                             -1 if up_variant is None else up_variant,
-                            -1 if down_variant is None else down_variant)
+                            -1 if down_variant is None else down_variant, m=problem.m)
     up = _tile(native.up_bm, native.up_bn, native.up_bk, native.up_variant)
     down = _tile(native.down_bm, native.down_bn, native.down_bk, native.down_variant)
     if selection.down_impl == "streamk":

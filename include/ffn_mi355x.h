@@ -49,6 +49,7 @@ extern "C" {
 /* Tile geometry and launch shape the library chose for one FFN.  It is the
  * counterpart of the reference's Plan/Tile (ops/host/tiling.py:11-74). */
 typedef struct ffn_mi355x_plan {
+    int m;                       /* logical rows of X (rows m..mp-1 are zero padding) */
     int mp, kp, hp, np;          /* padded extents the plan was made for */
     int dtype, down_impl, gelu;
     int block_num;               /* persistent workgroups per launch (<= CU count) */
@@ -74,8 +75,10 @@ int ffn_mi355x_query(int device, int* cu_count, char* arch, int arch_len);
  * full-load down variants (ops/host/dispatch.py:61-66), FFN_MI355X_EINVAL for a
  * block_num outside [1, 65535], FFN_MI355X_ENOT_APPLICABLE for Stream-K shapes
  * with no remainder tiles or fewer than two H iterations (tiling.py:65-70).
- * up_variant / down_variant < 0 let the library choose; >= 0 forces a tile. */
-int ffn_mi355x_make_plan(int mp, int kp, int hp, int np, int dtype, int down_impl,
+ * up_variant / down_variant < 0 let the library choose; >= 0 forces a tile.
+ * m is the logical row count: the zero-padding rows of X and hidden are then
+ * never fetched (they read as zeros), which matters for small-M decode shapes. */
+int ffn_mi355x_make_plan(int m, int mp, int kp, int hp, int np, int dtype, int down_impl,
                          int gelu, int block_num, int up_variant, int down_variant,
                          ffn_mi355x_plan* plan);
 
