@@ -28,6 +28,7 @@
 namespace ffn {
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((__vector_size__(16)));
@@ -95,10 +96,18 @@ struct TileCfg {
 // small device helpers
 // ---------------------------------------------------------------------------
 
+// Buffer descriptor of `bytes` bytes at `base`; both must be uniform over the wave.  They are
+// passed through readfirstlane so the descriptor is built in SGPRs: a descriptor the compiler
+// holds in VGPRs costs a waterfall loop (readfirstlane, compare, exec mask, branch) around every
+// load that uses it, which also splits the hand-interleaved MFMA schedule into basic blocks.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+    const int n = __builtin_amdgcn_readfirstlane((int)bytes);
+    void* ptr = (void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
     // word3 0x00020000: raw (untyped) 32-bit data format, range-checked against `bytes`
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
-                                             0x00020000);
+    return __builtin_amdgcn_make_buffer_rsrc(ptr, (short)0, n, 0x00020000);
 }
 
 // s_waitcnt vmcnt(n) with lgkm/exp counters left alone (gfx9 encoding).
@@ -118,22 +127,31 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
                                                       __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
+// Bit reinterpretation of one 32-bit value, taken by value: __builtin_bit_cast applied
+// directly to an element of an ext_vector_type (v.y, acc[k]) reads element 0 of the vector
+// instead, so elements always go through these.
+__device__ __forceinline__ float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
+__device__ __forceinline__ uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
+
 // Round-to-nearest-even FP32 -> storage type, four values packed into 8 bytes.
 template <int DT>
-__device__ __forceinline__ uint2 pack4(float a, float b, float c, float d) {
+__device__ __forceinline__ u32x2 pack4(float a, float b, float c, float d) {
+    uint16_t h0, h1, h2, h3;
     if constexpr (DT == DT_BF16) {
-        __bf16 h0 = (__bf16)a, h1 = (__bf16)b, h2 = (__bf16)c, h3 = (__bf16)d;
-        uint2 r;
-        r.x = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-        r.y = (uint32_t)__builtin_bit_cast(uint16_t, h2) | ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16);
-        return r;
+        h0 = __builtin_bit_cast(uint16_t, (__bf16)a);
+        h1 = __builtin_bit_cast(uint16_t, (__bf16)b);
+        h2 = __builtin_bit_cast(uint16_t, (__bf16)c);
+        h3 = __builtin_bit_cast(uint16_t, (__bf16)d);
     } else {
-        _Float16 h0 = (_Float16)a, h1 = (_Float16)b, h2 = (_Float16)c, h3 = (_Float16)d;
-        uint2 r;
-        r.x = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-        r.y = (uint32_t)__builtin_bit_cast(uint16_t, h2) | ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16);
-        return r;
+        h0 = __builtin_bit_cast(uint16_t, (_Float16)a);
+        h1 = __builtin_bit_cast(uint16_t, (_Float16)b);
+        h2 = __builtin_bit_cast(uint16_t, (_Float16)c);
+        h3 = __builtin_bit_cast(uint16_t, (_Float16)d);
     }
+    u32x2 r;
+    r.x = (uint32_t)h0 | ((uint32_t)h1 << 16);
+    r.y = (uint32_t)h2 | ((uint32_t)h3 << 16);
+    return r;
 }
 
 // ---------------------------------------------------------------------------
@@ -310,60 +328,79 @@ struct Engine {
         rb = make_rsrc(bbase, (uint32_t)min(C::BN, p.N - col0) * (uint32_t)ldb2);
     }
 
-    // DMA source offsets of this lane for K-iteration `kit` (even and odd blocks).  Chunks past
-    // K get an offset >= 2^31, beyond any range, and read as zero (rows past the operand are
-    // out of range of the tile's descriptor).  The whole offset travels in the VGPR operand:
-    // the buffer range check covers voffset but not soffset.
-    struct DmaOff {
+    // Per-lane DMA addressing, computed once per unit.  The lane fills physical chunk pc of
+    // row rl of every 1 KiB block, i.e. logical chunk pc ^ swz(row); the swizzle of a block's
+    // rows depends only on the block's parity.  a/b: byte offset of that chunk inside a block
+    // at K offset 0; kk: its first K element.
+    struct DmaLane {
         uint32_t a[2], b[2];
+        int kk[2];
     };
-    __device__ __forceinline__ DmaOff dma_offsets(const GemmParams& p, int kit) const {
-        // recomputed from an opaque lane id at every use: held across the persistent loop these
-        // per-lane constants get spilled, and each reload drains the outstanding DMA
+    __device__ __forceinline__ DmaLane dma_lane(const GemmParams& p) const {
+        // from an opaque lane id: the values depend only on the thread and would otherwise be
+        // hoisted out of the persistent loop and held (spilled) across the epilogue
         int ln = lane;
         asm volatile("" : "+v"(ln));
         const int rl = ln / C::CH, pc = ln % C::CH;
-        DmaOff o;
-        const int k0 = kit * C::BK;
+        DmaLane d;
 #pragma unroll
-        for (int par = 0; par < C::SWZ_PERIOD; ++par) {
-            // this lane fills physical chunk pc of row rl of each 1 KiB block, i.e. logical chunk
-            // pc ^ swz(row); the swizzle of a block's rows depends only on the block's parity
-            const int kk = (pc ^ swz_of(par * C::RPB + rl)) * 8;
-            const bool ok = (k0 + C::BK <= p.K) || (k0 + kk < p.K);
-            o.a[par] = ok ? (uint32_t)(rl * p.lda * 2 + (k0 + kk) * 2) : 0x80000000u;
-            o.b[par] = ok ? (uint32_t)(rl * p.ldb * 2 + (k0 + kk) * 2) : 0x80000000u;
+        for (int par = 0; par < 2; ++par) {
+            const int kk = (pc ^ swz_of((par % C::SWZ_PERIOD) * C::RPB + rl)) * 8;
+            d.kk[par] = kk;
+            d.a[par] = (uint32_t)(rl * p.lda * 2 + kk * 2);
+            d.b[par] = (uint32_t)(rl * p.ldb * 2 + kk * 2);
         }
-        if constexpr (C::SWZ_PERIOD == 1) o.a[1] = o.a[0], o.b[1] = o.b[0];
-        return o;
+        return d;
+    }
+    // Per-iteration scalars: the K byte offset of K-iteration kit, and the number of K elements
+    // left from there (0 for an iteration past the unit, whose DMA then reads only zeros).
+    struct DmaIt {
+        uint32_t k0x2;
+        int lim;
+    };
+    __device__ __forceinline__ DmaIt dma_it(const GemmParams& p, int kit, bool real) const {
+        DmaIt t;
+        t.k0x2 = (uint32_t)(kit * C::BK * 2);
+        t.lim = real ? p.K - kit * C::BK : 0;
+        return t;
     }
 
-    // DMA instruction D (of the LOADS this wave issues per stage) into LDS stage `stage`.
+    // DMA instruction D (of the LOADS this wave issues per stage) into LDS stage `stage`.  A
+    // chunk at or past K (and every chunk of an empty iteration) gets an offset >= 2^31, beyond
+    // any range, and reads as zero without a memory access; rows past the operand are out of
+    // range of the tile's descriptor.  The whole offset travels in the VGPR operand: the buffer
+    // range check covers voffset but not soffset.
     template <int D>
     __device__ __forceinline__ void issue_one(const GemmParams& p, const __amdgpu_buffer_rsrc_t& ra,
                                               const __amdgpu_buffer_rsrc_t& rb, int stage,
-                                              const DmaOff& o) const {
+                                              const DmaLane& L, const DmaIt& t) const {
         lds_char* st = smem + stage * C::STAGE_BYTES;
         if constexpr (D < C::A_PW) {
             const int blk = wave * C::A_PW + D;
+            constexpr int par = D & 1;
+            const uint32_t off = L.kk[par] < t.lim
+                                     ? L.a[par] + (uint32_t)blk * (uint32_t)(C::RPB * p.lda * 2) + t.k0x2
+                                     : 0x80000000u;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                ra, (__attribute__((address_space(3))) void*)(st + blk * 1024), 16,
-                (int)(o.a[D & 1] + (uint32_t)blk * (uint32_t)(C::RPB * p.lda * 2)), 0, 0, 0);
+                ra, (__attribute__((address_space(3))) void*)(st + blk * 1024), 16, (int)off, 0, 0, 0);
         } else {
             const int blk = wave * C::B_PW + (D - C::A_PW);
+            constexpr int par = (D - C::A_PW) & 1;
+            const uint32_t off = L.kk[par] < t.lim
+                                     ? L.b[par] + (uint32_t)blk * (uint32_t)(C::RPB * p.ldb * 2) + t.k0x2
+                                     : 0x80000000u;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rb, (__attribute__((address_space(3))) void*)(st + C::A_BYTES + blk * 1024), 16,
-                (int)(o.b[(D - C::A_PW) & 1] + (uint32_t)blk * (uint32_t)(C::RPB * p.ldb * 2)), 0, 0, 0);
+                rb, (__attribute__((address_space(3))) void*)(st + C::A_BYTES + blk * 1024), 16, (int)off, 0, 0, 0);
         }
     }
 
     template <int D0, int D1>
     __device__ __forceinline__ void issue_range(const GemmParams& p, const __amdgpu_buffer_rsrc_t& ra,
                                                 const __amdgpu_buffer_rsrc_t& rb, int stage,
-                                                const DmaOff& o) const {
+                                                const DmaLane& L, const DmaIt& t) const {
         if constexpr (D0 < D1) {
-            issue_one<D0>(p, ra, rb, stage, o);
-            issue_range<D0 + 1, D1>(p, ra, rb, stage, o);
+            issue_one<D0>(p, ra, rb, stage, L, t);
+            issue_range<D0 + 1, D1>(p, ra, rb, stage, L, t);
         }
     }
 
@@ -372,9 +409,10 @@ struct Engine {
     __device__ __forceinline__ void prologue(const GemmParams& p, const Unit& u) const {
         __amdgpu_buffer_rsrc_t ra, rb;
         rsrc(p, u, ra, rb);
+        const DmaLane L = dma_lane(p);
 #pragma unroll
         for (int s = 0; s < S - 1; ++s)
-            if (u.kb + s < u.ke) issue_range<0, C::LOADS>(p, ra, rb, s, dma_offsets(p, u.kb + s));
+            if (u.kb + s < u.ke) issue_range<0, C::LOADS>(p, ra, rb, s, L, dma_it(p, u.kb + s, true));
     }
 
     // Fragment registers: A (activation rows) double-buffered across k-steps, B (weight rows)
@@ -433,10 +471,19 @@ struct Engine {
                                               : (KS - 1) * NM + SYNC_Q;
     static_assert(KS >= 2 && DMA_SLOTS >= 1, "at least two k-steps per stage");
 
+    template <int Q, int JJ>
+    __device__ __forceinline__ void reload_b_at(int stage) {
+        if constexpr (JJ < FN) {
+            constexpr int last_use = JJ * FM + FM - 1;
+            if constexpr ((last_use > SYNC_Q ? last_use : SYNC_Q) == Q) read_b<JJ>(stage, 0);
+            reload_b_at<Q, JJ + 1>(stage);
+        }
+    }
+
     template <int CB, int MODE, bool DMA, int KSI, int Q>
     __device__ __forceinline__ void slot(const GemmParams& p, f32x16 (&acc)[FN][FM], int cur, int nxt,
                                          const __amdgpu_buffer_rsrc_t& ra, const __amdgpu_buffer_rsrc_t& rb,
-                                         int dma_stage, const DmaOff& o, const Unit& nx) {
+                                         int dma_stage, const DmaLane& L, const DmaIt& o, const Unit& nx) {
         constexpr int j = Q / FM, i = Q % FM;
         acc[j][i] = mfma32<DT>(fb[j], fa[CB][i], acc[j][i]);
         constexpr int NB = 1 - CB;
@@ -463,13 +510,15 @@ struct Engine {
                 constexpr int span = NM - SYNC_Q, qq = Q - SYNC_Q;
                 constexpr int a0 = qq * FM / span, a1 = (qq + 1) * FM / span;
                 read_a_range<NB, a0, a1>(nxt, 0);
-                if constexpr (i == FM - 1) read_b<j>(nxt, 0);
+                // B fragment jj is reloaded once both its last use (the end of block jj) and
+                // the barrier are behind
+                reload_b_at<Q, 0>(nxt);
             }
         }
         constexpr int g = KSI * NM + Q;  // this slot's share of the refill DMA
         if constexpr (DMA && g < DMA_SLOTS && (KSI + 1 < KS || Q < SYNC_Q)) {
             constexpr int t0 = g * C::LOADS / DMA_SLOTS, t1 = (g + 1) * C::LOADS / DMA_SLOTS;
-            issue_range<t0, t1>(p, ra, rb, dma_stage, o);
+            issue_range<t0, t1>(p, ra, rb, dma_stage, L, o);
         }
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -477,10 +526,10 @@ struct Engine {
     template <int CB, int MODE, bool DMA, int KSI, int Q>
     __device__ __forceinline__ void slots(const GemmParams& p, f32x16 (&acc)[FN][FM], int cur, int nxt,
                                           const __amdgpu_buffer_rsrc_t& ra, const __amdgpu_buffer_rsrc_t& rb,
-                                          int dma_stage, const DmaOff& o, const Unit& nx) {
+                                          int dma_stage, const DmaLane& L, const DmaIt& o, const Unit& nx) {
         if constexpr (Q < NM) {
-            slot<CB, MODE, DMA, KSI, Q>(p, acc, cur, nxt, ra, rb, dma_stage, o, nx);
-            slots<CB, MODE, DMA, KSI, Q + 1>(p, acc, cur, nxt, ra, rb, dma_stage, o, nx);
+            slot<CB, MODE, DMA, KSI, Q>(p, acc, cur, nxt, ra, rb, dma_stage, L, o, nx);
+            slots<CB, MODE, DMA, KSI, Q + 1>(p, acc, cur, nxt, ra, rb, dma_stage, L, o, nx);
         }
     }
 
@@ -488,21 +537,21 @@ struct Engine {
     __device__ __forceinline__ void ksteps(const GemmParams& p, const Unit& nx,
                                            const __amdgpu_buffer_rsrc_t& ra,
                                            const __amdgpu_buffer_rsrc_t& rb, int cur, int dstage,
-                                           const DmaOff& o, f32x16 (&acc)[FN][FM]) {
+                                           const DmaLane& L, const DmaIt& o, f32x16 (&acc)[FN][FM]) {
         if constexpr (KSI < KS) {
             constexpr int MODE = (KSI + 1 < KS) ? 0 : (LAST ? 2 : 1);
             const int nxt = (cur + 1 == S) ? 0 : cur + 1;
             // the last iteration of a unit refills nothing (its DMA prologue for the next unit
             // is issued after the barrier of its last k-step)
-            slots<KSI & 1, MODE, !LAST, KSI, 0>(p, acc, cur, nxt, ra, rb, dstage, o, nx);
-            ksteps<LAST, KSI + 1>(p, nx, ra, rb, cur, dstage, o, acc);
+            slots<KSI & 1, MODE, !LAST, KSI, 0>(p, acc, cur, nxt, ra, rb, dstage, L, o, nx);
+            ksteps<LAST, KSI + 1>(p, nx, ra, rb, cur, dstage, L, o, acc);
         }
     }
 
     // acc = sum over K-iterations [u.kb, u.ke) of tile (u.tm, u.tn).  On entry the DMA prologue
     // of the unit is in flight, possibly behind the previous unit's stores, so the first wait
     // drains everything.  Iteration it fetches iteration it+S-1 into the stage freed at the end
-    // of it-1; past the end of the unit it issues the same DMA against an empty descriptor
+    // of it-1; past the end of the unit it issues the same DMA with out-of-range offsets
     // (zeros into the free stage), which keeps every stage wait a compile-time count.  The
     // last iteration starts the DMA prologue of `nx`, which then overlaps this unit's epilogue.
     __device__ __forceinline__ void mainloop(const GemmParams& p, const Unit& u, const Unit& nx,
@@ -513,7 +562,7 @@ struct Engine {
             for (int i = 0; i < FM; ++i) acc[j][i] = f32x16{};
         __amdgpu_buffer_rsrc_t ra, rb;
         rsrc(p, u, ra, rb);
-        const __amdgpu_buffer_rsrc_t rnull = make_rsrc(p.a, 0);
+        const DmaLane L = dma_lane(p);
         const int n = u.ke - u.kb;
         wait_vmcnt<0>();
         barrier();
@@ -522,13 +571,12 @@ struct Engine {
         int cur = 0;
         for (int it = 0; it < n - 1; ++it) {
             const int dkit = it + S - 1;
-            const bool real = dkit < n;
-            const DmaOff o = dma_offsets(p, u.kb + dkit);
+            const DmaIt o = dma_it(p, u.kb + dkit, dkit < n);
             const int dstage = (cur == 0) ? S - 1 : cur - 1;
-            ksteps<false, 0>(p, nx, real ? ra : rnull, real ? rb : rnull, cur, dstage, o, acc);
+            ksteps<false, 0>(p, nx, ra, rb, cur, dstage, L, o, acc);
             cur = (cur + 1 == S) ? 0 : cur + 1;
         }
-        ksteps<true, 0>(p, nx, ra, rb, cur, 0, DmaOff{}, acc);
+        ksteps<true, 0>(p, nx, ra, rb, cur, 0, L, DmaIt{0u, 0}, acc);
     }
 
     // Output position of accumulator group (j, i, q): row m, columns n..n+3.
@@ -542,9 +590,9 @@ struct Engine {
     __device__ __forceinline__ void store4(const GemmParams& p, int m, int n, float v0, float v1,
                                            float v2, float v3) const {
         if (m < p.M && n < p.N) {
-            const uint2 v = pack4<DT>(activate<EPI>(v0), activate<EPI>(v1), activate<EPI>(v2),
+            const u32x2 v = pack4<DT>(activate<EPI>(v0), activate<EPI>(v1), activate<EPI>(v2),
                                       activate<EPI>(v3));
-            *(uint2*)((char*)p.c + ((size_t)m * (size_t)p.ldc + (size_t)n) * 2) = v;
+            *(u32x2*)((char*)p.c + ((size_t)m * (size_t)p.ldc + (size_t)n) * 2) = v;
         }
     }
 
@@ -598,6 +646,25 @@ struct Engine {
         int ln = lane, td = tid;
         asm volatile("" : "+v"(ln));
         asm volatile("" : "+v"(td));
+        // Pass 1, every wave busy: activate and cast the whole wave tile in registers; group
+        // (j, i, q) packs into words 2q, 2q+1 of acc[j][i], whose sources are already consumed.
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const u32x2 v = pack4<DT>(activate<EPI>(acc[j][i][4 * q]),
+                                              activate<EPI>(acc[j][i][4 * q + 1]),
+                                              activate<EPI>(acc[j][i][4 * q + 2]),
+                                              activate<EPI>(acc[j][i][4 * q + 3]));
+                    acc[j][i][2 * q] = u2f(v.x);
+                    acc[j][i][2 * q + 1] = u2f(v.y);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        // Pass 2: stage ER rows at a time through LDS and copy them out with full-row stores.
 #pragma unroll
         for (int c = 0; c < C::BM / ER; ++c) {
             barrier();
@@ -611,10 +678,9 @@ struct Engine {
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         const int nt = wn * C::WTN + 32 * j + 8 * q + 4 * (ln >> 5);
-                        const uint2 v = pack4<DT>(activate<EPI>(acc[j][i][4 * q]),
-                                                  activate<EPI>(acc[j][i][4 * q + 1]),
-                                                  activate<EPI>(acc[j][i][4 * q + 2]),
-                                                  activate<EPI>(acc[j][i][4 * q + 3]));
+                        u32x2 v;
+                        v.x = f2u(acc[j][i][2 * q]);
+                        v.y = f2u(acc[j][i][2 * q + 1]);
                         *(__attribute__((address_space(3))) unsigned long long*)(eb + rl * OUT_STRIDE + nt * 2) =
                             __builtin_bit_cast(unsigned long long, v);
                     }
@@ -710,8 +776,8 @@ __global__ void __launch_bounds__(C::NT) ffn_sk_reduce_kernel(GemmParams p, int 
         const int m = tm * C::BM + wm * C::WTM + 32 * i + (lane & 31);
         const int n = tn * C::BN + wn * C::WTN + 32 * j + 8 * q + 4 * (lane >> 5);
         if (m < p.M && n < p.N) {
-            const uint2 v = pack4<DT>(tot.x, tot.y, tot.z, tot.w);
-            *(uint2*)((char*)p.c + ((size_t)m * (size_t)p.ldc + (size_t)n) * 2) = v;
+            const u32x2 v = pack4<DT>(tot.x, tot.y, tot.z, tot.w);
+            *(u32x2*)((char*)p.c + ((size_t)m * (size_t)p.ldc + (size_t)n) * 2) = v;
         }
     }
 }

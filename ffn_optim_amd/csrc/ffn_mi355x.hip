@@ -73,21 +73,23 @@ long long cdiv(long long a, long long b) { return (a + b - 1) / b; }
 // where an iteration is bounded by the tile's MFMA rate and by the loads the workgroup can
 // keep in flight ((S-1) stages over the memory latency), and the whole GEMM by streaming
 // its operands from HBM once.  Rates are measured on MI355X (sustained clock ~1.8-2 GHz).
-constexpr double kCuMfmaRate = 4.5e12;     // FLOP/s per CU a 256x256 tile sustains
+constexpr double kCuMfmaRate = 4.8e12;     // FLOP/s per CU a 256x256 tile sustains
 constexpr double kCuLoadRate = 60e9;       // B/s per CU of LDS-DMA alongside MFMA work
-constexpr double kLoadLatency = 1.5e-6;    // s, HBM-miss load latency under load
+constexpr double kLoadLatency = 0.8e-6;    // s, L2/MALL load latency under load
 constexpr double kHbmRate = 6.5e12;        // B/s sustained HBM read rate
 constexpr double kLaunch = 3e-6;           // s, one extra kernel launch (Stream-K fixup)
 constexpr double kReduceRate = 3.0e12;     // B/s of the fixup kernel
+constexpr double kUnitOverhead = 2.5e-6;   // s per unit: DMA prologue latency + epilogue
 
-// Relative MFMA efficiency of each macro tile (measured, 256x256 = 1).
+// Relative MFMA efficiency of each macro tile (measured on the FFN shapes, 256x256 = 1): the
+// fragment reads per MFMA grow as the wave tile shrinks.
 double tile_eff(const Variant& v) {
-    const double intensity = (double)v.bm * v.bn / (double)(v.bm + v.bn);
-    double e = intensity >= 128.0 ? 1.0 : intensity / 128.0;
-    if (v.bm == 256 && v.bn == 128) e = 0.97;
-    if (v.bm == 128 && v.bn == 256) e = 0.97;
-    if (v.bm == 128 && v.bn == 128) e = 0.63;
-    return e;
+    const int a = v.bm < v.bn ? v.bm : v.bn, b = v.bm < v.bn ? v.bn : v.bm;
+    if (a >= 256) return 1.0;
+    if (a == 128 && b == 256) return 0.95;
+    if (a == 128) return 0.6;
+    if (a == 64 && b >= 128) return 0.42;
+    return 0.25;
 }
 
 // Seconds per BK-deep iteration of one workgroup on a tile with `rows` data-bearing rows.
@@ -106,7 +108,8 @@ long long rows_in_tile(const Variant& v, long long m_valid) { return std::min<lo
 double cost_basic(const Variant& v, long long M, long long m_valid, long long N, long long K, int G) {
     const long long T = cdiv(M, v.bm) * cdiv(N, v.bn);
     const long long waves = cdiv(T, G);
-    const double t = (double)waves * (double)cdiv(K, v.bk) * iter_time(v, rows_in_tile(v, m_valid));
+    const double t = (double)waves * ((double)cdiv(K, v.bk) * iter_time(v, rows_in_tile(v, m_valid)) +
+                                      kUnitOverhead);
     const double hbm = (double)(N * K + m_valid * K) * 2.0 / kHbmRate;
     return std::max(t, hbm);
 }
@@ -134,7 +137,8 @@ double cost_streamk(const Variant& v, const SkShape& s, long long m_valid, long 
     const double it = iter_time(v, rows_in_tile(v, m_valid));
     const long long dp_waves = cdiv(s.dp, G);
     const long long sk_iters = s.q + (s.r ? 1 : 0);
-    double t = it * ((double)dp_waves * s.k_iters + (double)sk_iters);
+    double t = it * ((double)dp_waves * s.k_iters + (double)sk_iters) +
+               kUnitOverhead * (double)(dp_waves + 1);
     // shared split tiles: FP32 partials written, re-read and reduced by a second launch
     const long long pieces_per_tile = std::min<long long>(G, cdiv(s.k_iters, std::max<long long>(1, s.q)) + 1);
     if (s.k_iters > sk_iters) {
