@@ -40,6 +40,9 @@ def parse_args(argv=None):
     p.add_argument("--no-extra", action="store_true", help="headline workload only")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU oracle time budget")
+    p.add_argument("--counters", action="store_true",
+                   help="untimed pass for rocprofv3 --pmc: a copy of known size (calibration), "
+                        "then each kernel of the workload's paths three times")
     return p.parse_args(argv)
 
 
@@ -114,12 +117,14 @@ def measure_path(case, down, steps, warmup, inputs):
 
 
 def traffic_from_profiles(kernel_tag, case_id):
-    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by a
-    copy-kernel calibration), read from the committed summary if one exists."""
-    path = REPO / "profiles" / f"traffic_{kernel_tag}_{case_id}.md"
+    """HBM-side bytes per launch of one kernel role, measured with rocprofv3 --pmc (FETCH_SIZE and
+    WRITE_SIZE, each scaled by what the counter reads for a copy of known size), read from the
+    committed summary profiles/traffic_<case>.md if one exists."""
+    path = REPO / "profiles" / f"traffic_{case_id}.md"
     if not path.exists():
         return None
-    m = re.search(r"^hbm_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text(), re.M)
+    m = re.search(r"^hbm_bytes_per_launch\[" + re.escape(kernel_tag) + r"\]:\s*([0-9.eE+]+)",
+                  path.read_text(), re.M)
     return float(m.group(1)) if m else None
 
 
@@ -154,6 +159,55 @@ def cpu_baseline(case, budget_s):
                       f"{sum(samples):.1f} s total) with torch FP32 on {threads} threads, {cpu}"}
 
 
+COPY_BYTES = 512 << 20   # calibration copy: reads and writes exactly this many bytes
+
+
+def counters_pass(case):
+    """Launch sequence for a counter run: the calibration copy (torch's elementwise copy kernel
+    over COPY_BYTES, so FETCH_SIZE/WRITE_SIZE of a kernel with known traffic can be read off),
+    then up and down of both down paths, three times each, untimed."""
+    import ctypes
+    import torch
+    from ffn_optim_amd import _lib, prepare_ffn
+    from ffn_optim_amd.cases import make_inputs
+    src = torch.ones(COPY_BYTES // 4, device="cuda", dtype=torch.float32)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    x, w1, w2 = make_inputs(case, "cuda")
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    for down in ("basic", "streamk"):
+        try:
+            prepared = prepare_ffn(x, w1, w2, down_impl=down)
+        except ValueError:
+            continue
+        plan = prepared.plan.native
+        xs, w1s, w2s, hid, out, ws = prepared.tensors
+        for _ in range(3):
+            lib.ffn_mi355x_up(ctypes.byref(plan), xs, w1s, hid, stream)
+        for _ in range(3):
+            lib.ffn_mi355x_down(ctypes.byref(plan), hid, w2s, out, ws, stream)
+        torch.cuda.synchronize()
+        print(f"counters pass: {case['case_id']} {down} up v{plan.up_variant} down v{plan.down_variant}",
+              flush=True)
+
+
+def cold_step_time(case, down, steps, inputs):
+    """Per-step time with the 256 MiB MALL and the L2s flushed before every step (a 1 GiB
+    scratch buffer is read between steps, which leaves only clean lines behind), for shapes
+    whose weights would otherwise stay cached."""
+    import torch
+    from ffn_optim_amd import prepare_ffn
+    x, w1, w2 = inputs
+    prepared = prepare_ffn(x, w1, w2, down_impl=down)
+    scratch = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+    t = time_events(prepared.run, steps, 3, flush=lambda: scratch.sum())
+    del scratch
+    return t
+
+
 def bench_case(case, steps, warmup):
     import torch
     from ffn_optim_amd.cases import make_inputs
@@ -178,8 +232,13 @@ def bench_case(case, steps, warmup):
             "up_tile": [prepared.plan.up.bm, prepared.plan.up.bn, prepared.plan.up.bk],
             "down_tile": [prepared.plan.down.bm, prepared.plan.down.bn, prepared.plan.down.bk],
             "block_num": prepared.plan.block_num,
+            "variants": [prepared.plan.up.variant, prepared.plan.down.variant],
         }
         del prepared
+        if case.get("memory_bound"):
+            cold = cold_step_time(case, down, min(steps, 20), inputs)
+            res[down].update(cold_ms_per_step=cold["median_ms"],
+                             cold_hbm_gbs=nums["bytes"] / cold["median_ms"] / 1e6)
     torch.cuda.synchronize()
     return nums, res
 
@@ -194,6 +253,9 @@ def main(argv=None):
     from ffn_optim_amd.cases import get_case
 
     case = get_case(args.case)
+    if args.counters:
+        counters_pass(case)
+        return 0
     nums, res = bench_case(case, args.steps, args.warmup)
     paths = {k: v for k, v in res.items() if "ms_per_step" in v}
     if not paths:

@@ -1,10 +1,12 @@
 """Case schema and deterministic inputs (restates common/cases.py).
 
 A case is a JSON object {case_id, shape, weight1_shape, weight2_shape, dtype,
-layout, seed, noncontiguous?, x_view?}; files carry schema_version 1
+layout, seed, noncontiguous?, x_view?, memory_bound?}; files carry schema_version 1
 (common/cases.py:7-25).  make_inputs draws the same seeded tensors as
 common/cases.py:34-50; x_view='transpose12' additionally gives X the strides of
 a dim-1/dim-2 transposed buffer with unchanged values (the unaligned 4-D case).
+memory_bound marks a workload judged on HBM bandwidth, which is also timed with the caches
+flushed between steps.
 """
 from __future__ import annotations
 
@@ -40,6 +42,8 @@ def load_cases(path):
             raise ValueError("noncontiguous must be boolean")
         if case.get("x_view") not in X_VIEWS:
             raise ValueError(f"x_view must be one of {X_VIEWS}")
+        if type(case.get("memory_bound", False)) is not bool:
+            raise ValueError("memory_bound must be boolean")
     return cases
 
 

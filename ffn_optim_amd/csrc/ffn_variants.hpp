@@ -1,8 +1,8 @@
 // ffn_variants.hpp -- the macro-tile variants compiled into libffn_mi355x.so.
 //
 // X(id, BM, BN, BK, waves along M, waves along N, LDS stages[, sync slot, DMA k-steps])
-// The deep-pipeline 64-row tiles (8, 9) keep 100+ KiB of loads in flight per CU for the
-// memory-bound small-M (decode) shapes.
+// The deep-pipeline 64-row tiles (8, 9) keep 56 KiB or more of weights in flight per CU for
+// the memory-bound small-M (decode) shapes.
 // Each variant is built for both storage types and four epilogues (GELU-erf,
 // GELU-rational, plain store, plain store + Stream-K split) in its own object.
 #pragma once
@@ -20,6 +20,7 @@
     X(9, 64, 128, 64, 2, 2, 6)
 
 #define FFN_NUM_VARIANTS 10
+
 
 // launch roles of one variant
 enum { FFN_ROLE_UP_ERF = 0, FFN_ROLE_UP_RATIONAL = 1, FFN_ROLE_DOWN_BASIC = 2, FFN_ROLE_DOWN_STREAMK = 3 };
