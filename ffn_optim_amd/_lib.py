@@ -55,8 +55,15 @@ _lib = None
 
 
 def load(path: Path | str | None = None):
-    """Load (once) and return the library; raises OSError if it cannot be loaded."""
+    """Load (once) and return the library; raises OSError if it cannot be loaded.
+
+    torch is imported first: it loads its own copy of the HIP runtime by path, and the
+    library's libamdhip64.so.7 dependency must then resolve (by soname) to that same copy.
+    Loaded the other way round, the process holds two HIP runtimes and the library's sees
+    no device once torch's owns it.  Importing torch initialises no GPU.
+    """
     global _lib
+    import torch  # noqa: F401  (HIP runtime load order, see above)
     with _lock:
         if _lib is None or path is not None:
             lib = ctypes.CDLL(str(path or LIBRARY_PATH), mode=ctypes.RTLD_LOCAL)

@@ -83,12 +83,14 @@ def _tile(bm, bn, bk, variant):
 
 
 def make_plan(problem, selection=Selection(), block_num=DEFAULT_BLOCK_NUM, *, gelu="erf",
-              up_variant=None, down_variant=None):
+              up_variant=None, down_variant=None, tuned=True):
     """Plan one FFN (ops/host/tiling.py:58-74).
 
     Raises DependencyUnavailable for full_load_*, ValueError for a block_num outside
     [1, 65535], NotApplicable when Stream-K has no remainder tiles for this
-    block_num or H spans fewer than two K iterations.
+    block_num or H spans fewer than two K iterations.  With neither variant forced
+    and tuned=True, a measured choice from the tuning table (ffn_optim_amd.tuning)
+    replaces the library planner's for the shapes it covers.
     """
     from .. import _lib
     from .dispatch import GELU_FORMS
@@ -101,6 +103,12 @@ def make_plan(problem, selection=Selection(), block_num=DEFAULT_BLOCK_NUM, *, ge
     mp, kp = align(problem.m, 64), align(problem.k, 16)
     hp, np_ = align(problem.h, 64), align(problem.n, 64)
     dtype = _lib.BF16 if problem.dtype == "bfloat16" else _lib.FP16
+    if tuned and up_variant is None and down_variant is None:
+        from .. import tuning
+        hit = tuning.lookup(tuning.make_key(problem.m, mp, kp, hp, np_, problem.dtype,
+                                            selection.down_impl, gelu, block_num))
+        if hit is not None:
+            up_variant, down_variant = hit
     native = _lib.make_plan(mp, kp, hp, np_, dtype, selection.down_impl, gelu, block_num,
                             -1 if up_variant is None else up_variant,
                             -1 if down_variant is None else down_variant, m=problem.m)

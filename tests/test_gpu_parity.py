@@ -5,6 +5,7 @@ the reference criterion compare() (mean_rel < 0.05, max_abs and rms reported),
 or bit-exactly where the arithmetic is exact (integer-valued operands).
 """
 import ctypes
+import json
 
 import pytest
 import torch
@@ -228,3 +229,24 @@ def test_up_integer_gelu_all_variants(dtype, kp):
                 tol = rational.abs() * eps + 1e-6 * z64.abs().float().clamp(min=1)
                 say("up-gelu", dtype, kp, gelu, variant, float(diff.max()))
                 assert bool((diff <= tol).all()), (gelu, variant)
+
+
+@pytest.mark.gpu
+def test_harness_manual_run_on_device(tmp_path):
+    """The measurement harness validates, times and profiles a case on the device."""
+    from ffn_optim_amd.performance.run import main
+    say("harness manual run, aligned_fp16, basic and streamk")
+    for down in ("basic", "streamk"):
+        root = tmp_path / down
+        assert main(["--execute-gpu", "--case-id", "aligned_fp16", "--down-impl", down, "--warmup", "1",
+                     "--repeats", "3", "--profile", "--output-root", str(root)]) == 0
+        run = next(root.iterdir())
+        rows = json.loads((run / "accuracy.json").read_text())
+        assert len(rows) == 1 and rows[0]["status"] == "passed", rows
+        row = rows[0]
+        assert row["device_median_us"] > 0 and len(row["device_samples_us"]) == 3
+        assert row["accuracy"]["mean_rel"] < 0.01
+        assert row["task_duration_us"] is None or row["task_duration_us"] > 0
+        assert row.get("profiler_path") or row.get("profiler_note")
+        assert json.loads((run / "manifest.json").read_text())["device_executed"]
+        assert json.loads((run / "best_configs.json").read_text())["aligned_fp16"]["configuration"]
