@@ -42,12 +42,12 @@ extern "C" hipError_t FFN_LAUNCHER(int role, const ffn::GemmParams* p, int grid,
         case FFN_ROLE_DOWN_STREAMK: {
             hipLaunchKernelGGL((ffn_gemm_kernel<FFN_DT, Cfg, EPI_STORE, true>), g, b, 0, stream, *p);
             if (p->sk_tiles > 0) {
-                // enough reduce workgroups to cover the chip, at most one per accumulator group
+                // one reduce workgroup per accumulator group of each split tile: every partial
+                // load of the fixup is then in flight at once (a workgroup walking several
+                // groups serialises their memory latencies)
                 constexpr int groups = Cfg::FN * Cfg::FM * 4;
-                int slices = (2 * grid + p->sk_tiles - 1) / p->sk_tiles;
-                slices = slices < 1 ? 1 : (slices > groups ? groups : slices);
-                hipLaunchKernelGGL((ffn_sk_reduce_kernel<FFN_DT, Cfg>), dim3(p->sk_tiles * slices), b, 0,
-                                   stream, *p, slices);
+                hipLaunchKernelGGL((ffn_sk_reduce_kernel<FFN_DT, Cfg>), dim3(p->sk_tiles * groups), b, 0,
+                                   stream, *p, groups);
             }
             break;
         }
