@@ -65,12 +65,14 @@ class PreparedFFN:
 
 
 def prepare_ffn(x, weight1, weight2, *, up_impl="basic", down_impl="basic", block_num=None,
-                layout="linear", gelu="erf", up_variant=None, down_variant=None):
+                layout="linear", gelu="erf", up_variant=None, down_variant=None, _alias=False):
     """Validate, plan, check the device, pad/contiguise and bind the kernels; no FFN launch.
 
     Follows ops/api.py:48-89.  Padding and contiguisation are auxiliary device
     operations timed outside the FFN.  up_variant/down_variant force a compiled
-    tile variant (tuning); None lets the library choose.
+    tile variant (tuning); None lets the library choose.  The prepared storage is a
+    snapshot of the inputs (later changes to x, weight1, weight2 do not reach run());
+    ffn() alone, which runs at once, may use aligned inputs in place (_alias).
     """
     from .host.dispatch import compile_kernel
     from . import _lib
@@ -92,7 +94,7 @@ def prepare_ffn(x, weight1, weight2, *, up_impl="basic", down_impl="basic", bloc
         stream = torch.cuda.current_stream()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
-        storage = prepare_storage(x, weight1, weight2, plan)
+        storage = prepare_storage(x, weight1, weight2, plan, alias_aligned=_alias)
         end.record()
         end.synchronize()
         auxiliary_ms = start.elapsed_time(end)
@@ -108,5 +110,10 @@ def prepare_ffn(x, weight1, weight2, *, up_impl="basic", down_impl="basic", bloc
 
 
 def ffn(x, weight1, weight2, **configuration):
-    """Y = GELU(X @ weight1.T) @ weight2.T; no bias, no autograd."""
-    return prepare_ffn(x, weight1, weight2, **configuration).run()
+    """Y = GELU(X @ weight1.T) @ weight2.T; no bias, no autograd (ops/api.py:92-94).
+
+    Operands that are contiguous with K, H and N already multiples of 16/64/64 are used
+    in place for this single launch instead of being copied into padded buffers; the
+    result is identical (the kernels read no padding rows and mask ragged tiles).
+    """
+    return prepare_ffn(x, weight1, weight2, **configuration, _alias=True).run()

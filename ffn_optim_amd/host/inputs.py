@@ -83,15 +83,30 @@ def validate_tensors(x, weight1, weight2, layout="linear", require_device=False)
                                str(x.dtype).removeprefix("torch."), layout)
 
 
-def prepare_storage(x, weight1, weight2, plan):
+def operands_aligned(x, weight1, weight2, plan):
+    """True when X, W1 and W2 can be used in place: contiguous, K, H and N already at their
+    padded widths.  M needs no padding: the kernels never read rows of X past m."""
+    p = plan.problem
+    return (p.k == plan.kp and p.h == plan.hp and p.n == plan.np and x.is_contiguous()
+            and weight1.is_contiguous() and weight2.is_contiguous())
+
+
+def prepare_storage(x, weight1, weight2, plan, alias_aligned=False):
     """Contiguise and zero-pad into [mp,kp], [hp,kp], [np,hp]; allocate hidden, out, workspace.
 
     Same buffers as ops/host/inputs.py:74-90; the FP32 workspace holds the Stream-K
-    partial tiles (every slot is written before it is read).
+    partial tiles (every slot is written before it is read).  With alias_aligned and
+    operands_aligned(), X ([m,kp] view), W1 and W2 are the caller's tensors themselves,
+    not copies: for a launch that runs before the caller can modify them.
     """
     import torch
 
     p = plan.problem
+    if alias_aligned and operands_aligned(x, weight1, weight2, plan):
+        hidden = torch.empty((plan.mp, plan.hp), device=x.device, dtype=x.dtype)
+        out = torch.empty((plan.mp, plan.np), device=x.device, dtype=x.dtype)
+        ws = torch.empty(plan.workspace_shape, device=x.device, dtype=torch.float32)
+        return x.view(p.m, p.k), weight1, weight2, hidden, out, ws
     xc = x.contiguous().view(p.m, p.k)
     w1c, w2c = weight1.contiguous(), weight2.contiguous()
     xp = torch.zeros((plan.mp, plan.kp), device=x.device, dtype=x.dtype)

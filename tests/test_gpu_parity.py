@@ -250,3 +250,34 @@ def test_harness_manual_run_on_device(tmp_path):
         assert row.get("profiler_path") or row.get("profiler_note")
         assert json.loads((run / "manifest.json").read_text())["device_executed"]
         assert json.loads((run / "best_configs.json").read_text())["aligned_fp16"]["configuration"]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", [((4, 25, 128), 256, 64), ((300, 1024), 512, 192), ((3, 37, 120), 200, 72)])
+def test_one_shot_ffn_in_place_matches_prepared(shape):
+    """ffn() on aligned inputs skips the padded copies; results are bit-identical to the
+    prepared (copied) path, and PreparedFFN keeps its snapshot of the inputs."""
+    from ffn_optim_amd import ffn
+    xs, h, n = shape
+    k = xs[-1]
+    say("one-shot ffn in place", xs, h, n)
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(*xs, generator=g).bfloat16().cuda()
+    w1 = (torch.randn(h, k, generator=g) * k ** -0.5).bfloat16().cuda()
+    w2 = (torch.randn(n, h, generator=g) * h ** -0.5).bfloat16().cuda()
+    for down in ("basic", "streamk"):
+        try:
+            prepared = prepare_ffn(x, w1, w2, down_impl=down)
+        except ValueError:
+            continue
+        ref = prepared.run().clone()
+        y = ffn(x, w1, w2, down_impl=down)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), down
+        res = compare(y.cpu(), ffn_torch(x.cpu(), w1.cpu(), w2.cpu()))
+        assert res["passed"], res
+        x.add_(1.0)                      # the prepared snapshot must not see this
+        again = prepared.run()
+        torch.cuda.synchronize()
+        assert torch.equal(again.view(torch.int16), ref.view(torch.int16))
+        x.sub_(1.0)

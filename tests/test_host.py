@@ -196,3 +196,31 @@ def test_case_schema_rejects_bad_files(tmp_path):
         bad.write_text(text)
         with pytest.raises(ValueError):
             load_cases(bad)
+
+
+def test_aligned_operands_used_in_place_only_when_asked():
+    import torch
+    from ffn_optim_amd.host.dispatch import Selection
+    from ffn_optim_amd.host.inputs import operands_aligned, prepare_storage, problem_from_shapes
+    from ffn_optim_amd.host.tiling import make_plan
+    g = torch.Generator().manual_seed(0)
+    # aligned K/H/N, ragged M (m=100): X is used as [m, kp] in place
+    x = torch.randn(4, 25, 128, generator=g).half()
+    w1, w2 = torch.randn(256, 128, generator=g).half(), torch.randn(64, 256, generator=g).half()
+    plan = make_plan(problem_from_shapes(x.shape, w1.shape, w2.shape, "float16"), Selection(), 8)
+    assert operands_aligned(x, w1, w2, plan)
+    xs, w1s, w2s, hid, out, ws = prepare_storage(x, w1, w2, plan, alias_aligned=True)
+    assert xs.data_ptr() == x.data_ptr() and xs.shape == (100, 128)
+    assert w1s is w1 and w2s is w2
+    assert hid.shape == (128, 256) and out.shape == (128, 64)
+    # without the request the storage is a padded snapshot
+    xs, w1s, _, _, _, _ = prepare_storage(x, w1, w2, plan)
+    assert xs.data_ptr() != x.data_ptr() and xs.shape == (128, 128)
+    assert torch.equal(xs[:100], x.view(100, 128)) and not xs[100:].any()
+    # unaligned K, or a non-contiguous X, is always copied and padded
+    for xx, ww1 in ((torch.randn(100, 120, generator=g).half(), torch.randn(256, 120, generator=g).half()),
+                    (x.transpose(0, 1), w1)):
+        p = make_plan(problem_from_shapes(xx.shape, ww1.shape, w2.shape, "float16"), Selection(), 8)
+        assert not operands_aligned(xx, ww1, w2, p)
+        xs = prepare_storage(xx, ww1, w2, p, alias_aligned=True)[0]
+        assert xs.data_ptr() != xx.data_ptr() and xs.shape == (p.mp, p.kp)
