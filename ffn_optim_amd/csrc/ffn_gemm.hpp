@@ -29,6 +29,9 @@ namespace ffn {
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((__vector_size__(16)));
@@ -133,24 +136,19 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
 __device__ __forceinline__ float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
 __device__ __forceinline__ uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
 
-// Round-to-nearest-even FP32 -> storage type, four values packed into 8 bytes.
+// Round-to-nearest-even FP32 -> storage type, four values packed into 8 bytes; each pair is
+// one v_cvt_pk_{bf16,f16}_f32.
 template <int DT>
 __device__ __forceinline__ u32x2 pack4(float a, float b, float c, float d) {
-    uint16_t h0, h1, h2, h3;
-    if constexpr (DT == DT_BF16) {
-        h0 = __builtin_bit_cast(uint16_t, (__bf16)a);
-        h1 = __builtin_bit_cast(uint16_t, (__bf16)b);
-        h2 = __builtin_bit_cast(uint16_t, (__bf16)c);
-        h3 = __builtin_bit_cast(uint16_t, (__bf16)d);
-    } else {
-        h0 = __builtin_bit_cast(uint16_t, (_Float16)a);
-        h1 = __builtin_bit_cast(uint16_t, (_Float16)b);
-        h2 = __builtin_bit_cast(uint16_t, (_Float16)c);
-        h3 = __builtin_bit_cast(uint16_t, (_Float16)d);
-    }
+    const f32x2 lo = {a, b}, hi = {c, d};
     u32x2 r;
-    r.x = (uint32_t)h0 | ((uint32_t)h1 << 16);
-    r.y = (uint32_t)h2 | ((uint32_t)h3 << 16);
+    if constexpr (DT == DT_BF16) {
+        r.x = __builtin_bit_cast(uint32_t, __builtin_convertvector(lo, bf16x2));
+        r.y = __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2));
+    } else {
+        r.x = __builtin_bit_cast(uint32_t, __builtin_convertvector(lo, f16x2));
+        r.y = __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, f16x2));
+    }
     return r;
 }
 
@@ -159,29 +157,33 @@ __device__ __forceinline__ u32x2 pack4(float a, float b, float c, float d) {
 // ---------------------------------------------------------------------------
 
 // Exact-form GELU, z * Phi(z) = 0.5*z*(1+erf(z/sqrt2)) -- F.gelu(approximate='none').
-// Phi is evaluated from erfc of |z|/sqrt2 (no cancellation in either tail):
-//     Phi(z) = 0.5*erfc(|z|/sqrt2)        for z < 0,   1 - 0.5*erfc(|z|/sqrt2)   otherwise,
-// with erfc from the Chebyshev fit of Press, Teukolsky, Vetterling & Flannery, "Numerical
-// Recipes in C" (2nd ed., sec. 6.2, erfcc; fractional error < 1.2e-7 for every x >= 0):
-//     erfc(x) = t*exp(-x*x + P(t)),  t = 1/(1 + x/2),  P a degree-9 polynomial.
-// The factor 1/2 and the change to base 2 are folded into the coefficients, so the whole
-// epilogue is one v_rcp_f32, one v_exp_f32 and about 18 full-rate VALU operations.
+// With h = Phi(-|z|) = 0.5*erfc(|z|/sqrt2), GELU(z) = max(z, 0) - |z|*h for either sign of z
+// (z >= 0: z*(1-h); z < 0: z*h), so one max and one FMA replace the sign select, and erfc
+// is only ever needed on the non-negative axis, where it has no cancellation.
+// erfc uses the form of the Chebyshev fit of Press, Teukolsky, Vetterling & Flannery,
+// "Numerical Recipes in C" (2nd ed., sec. 6.2, erfcc):
+//     erfc(x) = t*exp(-x*x + P(t)),  t = 1/(1 + x/2),
+// with P of degree 7 fitted here (Lawson-reweighted least squares of log(erfc(x)/t) + x^2 in t
+// over x in [0, 10.5]; past that erfc is below the FP32 subnormals): relative error 6.5e-7 in
+// float64 and ~5e-6 in FP32 evaluation, where the rounding of x*x dominates (the degree-9 fit
+// does no better in FP32).  1/sqrt2, the factor 1/2 of h and the change to base 2 are folded
+// into the constants: one v_rcp_f32, one v_exp_f32 and about 12 full-rate VALU ops.  Like the
+// torch golden it returns NaN for z = +-inf and NaN.
 __device__ __forceinline__ float gelu_erf(float z) {
-    constexpr float L2E = 1.4426950408889634f;                 // log2(e)
-    const float x = __builtin_fabsf(z) * 0.70710678118654752f;  // |z| / sqrt(2)
-    const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.5f, x, 1.0f));
-    float p = __builtin_fmaf(t, 0.17087277f * L2E, -0.82215223f * L2E);
-    p = __builtin_fmaf(t, p, 1.48851587f * L2E);
-    p = __builtin_fmaf(t, p, -1.13520398f * L2E);
-    p = __builtin_fmaf(t, p, 0.27886807f * L2E);
-    p = __builtin_fmaf(t, p, -0.18628806f * L2E);
-    p = __builtin_fmaf(t, p, 0.09678418f * L2E);
-    p = __builtin_fmaf(t, p, 0.37409196f * L2E);
-    p = __builtin_fmaf(t, p, 1.00002368f * L2E);
-    p = __builtin_fmaf(t, p, -1.26551223f * L2E - 1.0f);      // -1: the factor 1/2 of Phi
-    const float half = t * __builtin_amdgcn_exp2f(__builtin_fmaf(-x, x * L2E, p));
-    const float phi = z < 0.0f ? half : 1.0f - half;
-    return z * phi;
+    constexpr float L2E = 1.4426950408889634f;                  // log2(e)
+    const float a = __builtin_fabsf(z);
+    const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(a, 0.35355339059327376f, 1.0f));  // 1/(1+|z|/(2 sqrt2))
+    float p = __builtin_fmaf(t, -0.1845742772f * L2E, 0.7379936207f * L2E);
+    p = __builtin_fmaf(t, p, -0.9773950853f * L2E);
+    p = __builtin_fmaf(t, p, 0.3279841365f * L2E);
+    p = __builtin_fmaf(t, p, -0.0281352906f * L2E);
+    p = __builtin_fmaf(t, p, 0.3905195168f * L2E);
+    p = __builtin_fmaf(t, p, 0.9991159075f * L2E);
+    p = __builtin_fmaf(t, p, -1.2655091784f * L2E - 1.0f);     // -1: the factor 1/2 of h
+    const float h = t * __builtin_amdgcn_exp2f(__builtin_fmaf(-a, a * (0.5f * L2E), p));  // -x^2 = -z^2/2
+    // max(z, 0) as med3(z, 0, FLT_MAX): no NaN canonicalisation is needed, a NaN z already
+    // makes |z| and the result NaN
+    return __builtin_fmaf(-a, h, __builtin_amdgcn_fmed3f(z, 0.0f, 3.402823466e38f));
 }
 
 // Rational erf GELU: t = clamp(z/sqrt2, +-3.92), erf(t) ~ t*P5(t^2)/Q5(t^2), coefficients and
