@@ -85,6 +85,23 @@ struct TileCfg {
     static constexpr int LOADS = A_PW + B_PW;      // DMA instructions per wave per stage
     static constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
     static constexpr int KSTEPS = BK / 16;         // MFMA k-steps per stage
+    // Output staging of the epilogue: from stage STAGES-1 (which the next unit's DMA prologue
+    // leaves free) up to EPI_AVAIL bytes.  A workgroup whose stages take more than half of the
+    // LDS runs alone on its CU, so it may use all 160 KiB; a smaller one keeps to one stage and
+    // does not cut the number of workgroups per CU.  ER output rows are staged at a time: ER/WGM
+    // rows of every wave row (whole 32-row blocks), so that every wave writes every chunk.
+    static constexpr int LDS_MAX = 160 * 1024;
+    static constexpr int EPI_OFF = (STAGES - 1) * STAGE_BYTES;
+    static constexpr int EPI_AVAIL = (LDS_BYTES > LDS_MAX / 2) ? LDS_MAX - EPI_OFF : STAGE_BYTES;
+    static constexpr int OUT_ROWB = BN * 2;        // bytes of one staged output row (unpadded)
+    static constexpr int er_pick() {
+        for (int er = BM; er >= 32 * WGM; er /= 2)
+            if (BM % er == 0 && (er / WGM) % 32 == 0 && er * OUT_ROWB <= EPI_AVAIL) return er;
+        return 0;
+    }
+    static constexpr int ER = er_pick();
+    static constexpr int LDS_ALLOC = (EPI_OFF + ER * OUT_ROWB > LDS_BYTES) ? EPI_OFF + ER * OUT_ROWB : LDS_BYTES;
+    static_assert(ER > 0, "no output chunk of whole 32-row blocks fits the staging area");
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
     static_assert(ROWB % 16 == 0 && CH >= 2, "BK must be a multiple of 16");
     static_assert(A_BLKS % NW == 0 && B_BLKS % NW == 0, "DMA blocks must split evenly over waves");
@@ -92,7 +109,7 @@ struct TileCfg {
     static_assert(SWZ_PERIOD <= 2, "at most two DMA offset sets");
     static_assert(SWZ_PERIOD == 1 || (A_PW % 2 == 0 && B_PW % 2 == 0),
                   "block parity of every DMA instruction must be known at compile time");
-    static_assert(LDS_BYTES <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
+    static_assert(LDS_ALLOC <= LDS_MAX, "gfx950 has 160 KiB of LDS per CU");
 };
 
 // ---------------------------------------------------------------------------
@@ -623,37 +640,34 @@ struct Engine {
     // The accumulators of a lane cover 4 consecutive columns of 16 different rows, so storing
     // them directly writes every 128-byte output line in eight 16-byte pieces spread over time,
     // which the memory side pays for dearly.  Instead the tile is activated and cast in
-    // registers, written into LDS stage S-1 (the one the next unit's DMA prologue does not
-    // fill) in chunks of ER rows, and copied out with full-row 16-byte-per-lane stores.
-    static constexpr int OUT_STRIDE = C::BN * 2 + 16;  // LDS bytes per staged output row
-    static constexpr int ER_FIT = C::STAGE_BYTES / OUT_STRIDE;
-    static constexpr int ER = ER_FIT >= C::BM ? C::BM : (ER_FIT >= 128 ? 128 : (ER_FIT >= 64 ? 64 : 32));
-    static_assert(ER * OUT_STRIDE <= C::STAGE_BYTES && ER % 32 == 0 && C::BM % ER == 0,
-                  "an output chunk fits one LDS stage");
+    // registers, written into the staging area ER rows at a time, and copied out with full-row
+    // 16-byte-per-lane stores.  Staged rows are unpadded; the 16-byte chunk c of staged row s
+    // sits at c ^ ((s / RPW) mod OSWZ), RPW = rows per 256-byte bank line, which spreads the
+    // 32 rows of one ds_write_b64 and the chunks of one ds_read_b128 over all 64 banks.
+    static constexpr int ER = C::ER;
+    static constexpr int ERW = ER / C::WGM;              // rows of each wave row per chunk
+    static constexpr int BPC = ERW / 32;                 // 32-row blocks of a wave per chunk
+    static constexpr int NCH = C::BM / ER;               // chunks per tile
     static constexpr int TPR = C::BN / 8;                // 16-byte pieces per output row
+    static constexpr int RPW = C::OUT_ROWB >= 256 ? 1 : 256 / C::OUT_ROWB;
+    static constexpr int OSWZ = TPR < 16 ? TPR : 16;
     static constexpr int PIECES = ER * TPR / NT;         // pieces per thread per chunk
     static_assert((ER * TPR) % NT == 0, "chunk pieces split evenly over the threads");
+    static_assert(BPC >= 1 && FM % BPC == 0, "whole blocks per chunk");
 
+    static __device__ __forceinline__ int out_off(int s, int ch) {
+        return s * C::OUT_ROWB + ((ch ^ ((s / RPW) % OSWZ)) << 4);
+    }
+
+    // Activate and cast the blocks of chunk c in registers: group (j, i, q) packs into words
+    // 2q, 2q+1 of acc[j][i], whose sources are already consumed.
     template <int EPI>
-    __device__ __forceinline__ void store_tile_lds(const GemmParams& p, const Unit& u, bool next,
-                                                   f32x16 (&acc)[FN][FM]) {
-        lds_char* eb = smem + (S - 1) * C::STAGE_BYTES;
-        // DMA still in flight may target any stage but the next unit's prologue (issued last):
-        // drain it, then make sure every wave has, before the staging area is written
-        if (next) wait_vmcnt<C::LOADS * (S - 1)>();
-        else wait_vmcnt<0>();
-        const int row0 = u.tm * C::BM, col0 = u.tn * C::BN;
-        // opaque copies: the addressing below depends only on the thread id, and would
-        // otherwise be hoisted out of the persistent loop and held (spilled) across it
-        int ln = lane, td = tid;
-        asm volatile("" : "+v"(ln));
-        asm volatile("" : "+v"(td));
-        // Pass 1, every wave busy: activate and cast the whole wave tile in registers; group
-        // (j, i, q) packs into words 2q, 2q+1 of acc[j][i], whose sources are already consumed.
+    __device__ __forceinline__ void activate_chunk(int c, f32x16 (&acc)[FN][FM]) const {
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
+        for (int ib = 0; ib < BPC; ++ib) {
+            const int i = c * BPC + ib;
 #pragma unroll
-            for (int i = 0; i < FM; ++i) {
+            for (int j = 0; j < FN; ++j) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const u32x2 v = pack4<DT>(activate<EPI>(acc[j][i][4 * q]),
@@ -666,15 +680,32 @@ struct Engine {
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-        // Pass 2: stage ER rows at a time through LDS and copy them out with full-row stores.
+    }
+
+    template <int EPI>
+    __device__ __forceinline__ void store_tile_lds(const GemmParams& p, const Unit& u, bool next,
+                                                   f32x16 (&acc)[FN][FM]) {
+        lds_char* eb = smem + C::EPI_OFF;
+        // DMA still in flight may target any stage but the next unit's prologue (issued last):
+        // drain it; the barrier before the first staging write makes sure every wave has
+        if (next) wait_vmcnt<C::LOADS * (S - 1)>();
+        else wait_vmcnt<0>();
+        const int row0 = u.tm * C::BM, col0 = u.tn * C::BN;
+        // opaque copies: the addressing below depends only on the thread id, and would
+        // otherwise be hoisted out of the persistent loop and held (spilled) across it
+        int ln = lane, td = tid;
+        asm volatile("" : "+v"(ln));
+        asm volatile("" : "+v"(td));
+        activate_chunk<EPI>(0, acc);
 #pragma unroll
-        for (int c = 0; c < C::BM / ER; ++c) {
+        for (int c = 0; c < NCH; ++c) {
             barrier();
+            // staged row of this lane's rows in block (c*BPC + ib): wave row wm, local row
+            const int sr = wm * ERW + (ln & 31);
 #pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                const int rt = wm * C::WTM + 32 * i;  // first tile row of block i (wave-uniform)
-                if (rt / ER != c) continue;
-                const int rl = rt - c * ER + (ln & 31);
+            for (int ib = 0; ib < BPC; ++ib) {
+                const int i = c * BPC + ib;
+                const int s = sr + ib * 32;
 #pragma unroll
                 for (int j = 0; j < FN; ++j) {
 #pragma unroll
@@ -683,21 +714,31 @@ struct Engine {
                         u32x2 v;
                         v.x = f2u(acc[j][i][2 * q]);
                         v.y = f2u(acc[j][i][2 * q + 1]);
-                        *(__attribute__((address_space(3))) unsigned long long*)(eb + rl * OUT_STRIDE + nt * 2) =
+                        *(__attribute__((address_space(3))) unsigned long long*)(eb + out_off(s, nt >> 3) + (nt & 7) * 2) =
                             __builtin_bit_cast(unsigned long long, v);
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
             barrier();
+            // copy-out of chunk c: the LDS reads go first, the next chunk's activation runs
+            // while they land, then the stores
+            u32x4 v[PIECES];
 #pragma unroll
             for (int k = 0; k < PIECES; ++k) {
                 const int idx = k * NT + td;
-                const int r = idx / TPR, ch = idx - r * TPR;
-                const u32x4 v = *(const __attribute__((address_space(3))) u32x4*)(eb + r * OUT_STRIDE + ch * 16);
-                const int gm = row0 + c * ER + r, gn = col0 + ch * 8;
+                const int s = idx / TPR, ch = idx - s * TPR;
+                v[k] = *(const __attribute__((address_space(3))) u32x4*)(eb + out_off(s, ch));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (c + 1 < NCH) activate_chunk<EPI>(c + 1, acc);
+#pragma unroll
+            for (int k = 0; k < PIECES; ++k) {
+                const int idx = k * NT + td;
+                const int s = idx / TPR, ch = idx - s * TPR;
+                const int gm = row0 + (s / ERW) * C::WTM + c * ERW + (s % ERW), gn = col0 + ch * 8;
                 if (gm < p.M && gn < p.N)
-                    *(u32x4*)((char*)p.c + ((size_t)gm * (size_t)p.ldc + (size_t)gn) * 2) = v;
+                    *(u32x4*)((char*)p.c + ((size_t)gm * (size_t)p.ldc + (size_t)gn) * 2) = v[k];
             }
         }
     }
@@ -725,7 +766,7 @@ struct Engine {
 // Split pieces that share a tile publish FP32 partials; ffn_sk_reduce_kernel finishes them.
 template <int DT, class C, int EPI, bool SK>
 __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
-    __shared__ __attribute__((aligned(1024))) char smem_raw[C::LDS_BYTES];
+    __shared__ __attribute__((aligned(1024))) char smem_raw[C::LDS_ALLOC];
     Engine<DT, C> eng((lds_char*)smem_raw, p);
     f32x16 acc[C::FN][C::FM];
 

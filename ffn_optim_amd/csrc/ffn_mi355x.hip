@@ -37,13 +37,15 @@ namespace {
 
 struct Variant {
     int bm, bn, bk, wgm, wgn, stages;
+    int lds_bytes;            // LDS of one workgroup: the stages plus any epilogue staging beyond
     ffn_launch_fn launch[2];  // [dtype]
     int waves() const { return wgm * wgn; }
-    int lds() const { return stages * (bm + bn) * bk * 2; }
+    int lds() const { return lds_bytes; }
 };
 
-#define FFN_VARIANT_ROW(id, bm, bn, bk, wgm, wgn, st, ...) \
-    {bm, bn, bk, wgm, wgn, st, {ffn_launch_d0_v##id, ffn_launch_d1_v##id}},
+#define FFN_VARIANT_ROW(id, bm, bn, bk, wgm, wgn, st, ...)                                       \
+    {bm, bn, bk, wgm, wgn, st, ffn::TileCfg<bm, bn, bk, wgm, wgn, st, ##__VA_ARGS__>::LDS_ALLOC, \
+     {ffn_launch_d0_v##id, ffn_launch_d1_v##id}},
 const Variant kVariants[] = {FFN_VARIANTS(FFN_VARIANT_ROW)};
 #undef FFN_VARIANT_ROW
 constexpr int kNumVariants = (int)(sizeof(kVariants) / sizeof(kVariants[0]));
