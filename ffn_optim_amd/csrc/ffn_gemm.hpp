@@ -598,44 +598,6 @@ struct Engine {
         ksteps<true, 0>(p, nx, ra, rb, cur, 0, L, DmaIt{0u, 0}, acc);
     }
 
-    // Output position of accumulator group (j, i, q): row m, columns n..n+3.
-    __device__ __forceinline__ void group_pos(int tm, int tn, int j, int i, int q, int& m,
-                                              int& n) const {
-        m = tm * C::BM + wm * C::WTM + 32 * i + (lane & 31);
-        n = tn * C::BN + wn * C::WTN + 32 * j + 8 * q + 4 * (lane >> 5);
-    }
-
-    template <int EPI>
-    __device__ __forceinline__ void store4(const GemmParams& p, int m, int n, float v0, float v1,
-                                           float v2, float v3) const {
-        if (m < p.M && n < p.N) {
-            const u32x2 v = pack4<DT>(activate<EPI>(v0), activate<EPI>(v1), activate<EPI>(v2),
-                                      activate<EPI>(v3));
-            *(u32x2*)((char*)p.c + ((size_t)m * (size_t)p.ldc + (size_t)n) * 2) = v;
-        }
-    }
-
-    // Write acc (activated, cast) to C[tile] with row/column masking.  One 32x32 block at a
-    // time: the scheduling fences keep the compiler from moving all 256 accumulators into
-    // VGPRs at once (which would spill the long-lived addressing registers).
-    template <int EPI>
-    __device__ __forceinline__ void store_tile(const GemmParams& p, int tm, int tn,
-                                               f32x16 (&acc)[FN][FM]) const {
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-            for (int i = 0; i < FM; ++i) {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    int m, n;
-                    group_pos(tm, tn, j, i, q, m, n);
-                    store4<EPI>(p, m, n, acc[j][i][4 * q], acc[j][i][4 * q + 1],
-                                acc[j][i][4 * q + 2], acc[j][i][4 * q + 3]);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }
-    }
-
     // ---- epilogue through LDS --------------------------------------------------------------
     // The accumulators of a lane cover 4 consecutive columns of 16 different rows, so storing
     // them directly writes every 128-byte output line in eight 16-byte pieces spread over time,
@@ -652,6 +614,7 @@ struct Engine {
     static constexpr int RPW = C::OUT_ROWB >= 256 ? 1 : 256 / C::OUT_ROWB;
     static constexpr int OSWZ = TPR < 16 ? TPR : 16;
     static constexpr int PIECES = ER * TPR / NT;         // pieces per thread per chunk
+    static constexpr int PB = PIECES < 8 ? PIECES : 8;   // pieces in flight per thread
     static_assert((ER * TPR) % NT == 0, "chunk pieces split evenly over the threads");
     static_assert(BPC >= 1 && FM % BPC == 0, "whole blocks per chunk");
 
@@ -721,24 +684,66 @@ struct Engine {
                 }
             }
             barrier();
-            // copy-out of chunk c: the LDS reads go first, the next chunk's activation runs
-            // while they land, then the stores
-            u32x4 v[PIECES];
+            // copy-out of chunk c in batches of PB pieces: the LDS reads of a batch go first
+            // (with the next chunk's activation behind the first batch), then its stores
 #pragma unroll
-            for (int k = 0; k < PIECES; ++k) {
-                const int idx = k * NT + td;
-                const int s = idx / TPR, ch = idx - s * TPR;
-                v[k] = *(const __attribute__((address_space(3))) u32x4*)(eb + out_off(s, ch));
+            for (int k0 = 0; k0 < PIECES; k0 += PB) {
+                u32x4 v[PB];
+#pragma unroll
+                for (int k = 0; k < PB; ++k) {
+                    const int idx = (k0 + k) * NT + td;
+                    const int s = idx / TPR, ch = idx - s * TPR;
+                    v[k] = *(const __attribute__((address_space(3))) u32x4*)(eb + out_off(s, ch));
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if (k0 == 0 && c + 1 < NCH) activate_chunk<EPI>(c + 1, acc);
+#pragma unroll
+                for (int k = 0; k < PB; ++k) {
+                    const int idx = (k0 + k) * NT + td;
+                    const int s = idx / TPR, ch = idx - s * TPR;
+                    const int gm = row0 + (s / ERW) * C::WTM + c * ERW + (s % ERW), gn = col0 + ch * 8;
+                    if (gm < p.M && gn < p.N)
+                        *(u32x4*)((char*)p.c + ((size_t)gm * (size_t)p.ldc + (size_t)gn) * 2) = v[k];
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
-            __builtin_amdgcn_sched_barrier(0);
-            if (c + 1 < NCH) activate_chunk<EPI>(c + 1, acc);
+        }
+    }
+
+    // ---- epilogue straight from registers --------------------------------------------------
+    // Group q of a lane holds columns 8q + 4h + 0..3 of row (lane & 31), h = lane >> 5.  One
+    // v_permlane32_swap per word exchanges the high-lane words of group 2p with the low-lane
+    // words of group 2p+1, after which lane l < 32 holds columns 16p + 0..7 and lane l + 32
+    // columns 16p + 8..15 of the same row: every 32x32 block leaves in two 16-byte stores per
+    // lane (32 rows x 32 contiguous bytes per instruction), with no LDS round trip and no
+    // barrier, so the next unit's main loop starts as soon as the stores are issued.
+    template <int EPI>
+    __device__ __forceinline__ void store_tile_regs(const GemmParams& p, const Unit& u,
+                                                    f32x16 (&acc)[FN][FM]) const {
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int m0 = u.tm * C::BM + wm * C::WTM + (ln & 31);
+        const int n0 = u.tn * C::BN + wn * C::WTN + 8 * (ln >> 5);
 #pragma unroll
-            for (int k = 0; k < PIECES; ++k) {
-                const int idx = k * NT + td;
-                const int s = idx / TPR, ch = idx - s * TPR;
-                const int gm = row0 + (s / ERW) * C::WTM + c * ERW + (s % ERW), gn = col0 + ch * 8;
-                if (gm < p.M && gn < p.N)
-                    *(u32x4*)((char*)p.c + ((size_t)gm * (size_t)p.ldc + (size_t)gn) * 2) = v[k];
+        for (int i = 0; i < FM; ++i) {
+            const int m = m0 + 32 * i;
+            char* row = (char*)p.c + (size_t)m * (size_t)p.ldc * 2;
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                u32x2 g[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    g[q] = pack4<DT>(activate<EPI>(acc[j][i][4 * q]), activate<EPI>(acc[j][i][4 * q + 1]),
+                                     activate<EPI>(acc[j][i][4 * q + 2]), activate<EPI>(acc[j][i][4 * q + 3]));
+#pragma unroll
+                for (int pp = 0; pp < 2; ++pp) {
+                    const auto s0 = __builtin_amdgcn_permlane32_swap(g[2 * pp].x, g[2 * pp + 1].x, false, false);
+                    const auto s1 = __builtin_amdgcn_permlane32_swap(g[2 * pp].y, g[2 * pp + 1].y, false, false);
+                    const u32x4 v = {(uint32_t)s0[0], (uint32_t)s1[0], (uint32_t)s0[1], (uint32_t)s1[1]};
+                    const int n = n0 + 32 * j + 16 * pp;
+                    if (m < p.M && n < p.N) *(u32x4*)(row + (size_t)n * 2) = v;
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
     }
@@ -766,7 +771,13 @@ struct Engine {
 // Split pieces that share a tile publish FP32 partials; ffn_sk_reduce_kernel finishes them.
 template <int DT, class C, int EPI, bool SK>
 __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
-    __shared__ __attribute__((aligned(1024))) char smem_raw[C::LDS_ALLOC];
+    // The activation epilogue stores from registers, where its VALU work overlaps the stores;
+    // the plain cast stages through LDS, whose full-row stores drain faster when every
+    // workgroup stores at once.  The Stream-K kernel, whose split pieces leave through
+    // store_partial, stores its whole tiles from registers too: the staging registers would
+    // push it past 256 VGPRs.
+    constexpr bool EPI_IN_REGS = EPI != EPI_STORE || SK;
+    __shared__ __attribute__((aligned(1024))) char smem_raw[EPI_IN_REGS ? C::LDS_BYTES : C::LDS_ALLOC];
     Engine<DT, C> eng((lds_char*)smem_raw, p);
     f32x16 acc[C::FN][C::FM];
 
@@ -785,6 +796,8 @@ __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
         eng.mainloop(p, u, nx, acc);
         if (SK && u.split >= 0)
             eng.store_partial(sk_slot(p, v, u.local, C::BM * C::BN), acc);
+        else if constexpr (EPI_IN_REGS)
+            eng.template store_tile_regs<EPI>(p, u, acc);
         else
             eng.template store_tile_lds<EPI>(p, u, nx.valid, acc);
         if (!nx.valid) break;
