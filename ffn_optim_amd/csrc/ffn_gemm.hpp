@@ -57,6 +57,7 @@ struct GemmParams {
     int sk_q, sk_r;       // split iterations per workgroup: q, plus one for the first r
     int slots_per_wg;     // partial-tile slots owned by each workgroup
     int group_m;          // tile-order swizzle: tiles walk group_m tile-rows column by column
+    int fast_dma;         // 1: launch the kernel whose interior tiles refill through the SALU-addressed DMA path
 };
 
 // SYNCQ_: MFMA slot of a stage's last k-step after which the stage wait + barrier is placed
@@ -413,13 +414,41 @@ struct Engine {
         }
     }
 
-    template <int D0, int D1>
+    // The same DMA instruction for a full iteration of an interior tile: every row of the tile
+    // lies inside its operand and every chunk inside K, so no lane needs the zero-fill offset.
+    // The lane's VGPR offset is then a constant of the kernel and the row-block and K offsets
+    // travel in soffset (SALU arithmetic only): no vector instruction per DMA, which keeps the
+    // VALU out of the MFMA's way.  Every address is in bounds by construction, so this does
+    // not rely on the descriptor's range check.
+    template <int D>
+    __device__ __forceinline__ void issue_one_fast(const GemmParams& p, const __amdgpu_buffer_rsrc_t& ra,
+                                                   const __amdgpu_buffer_rsrc_t& rb, int stage,
+                                                   const DmaLane& L, const DmaIt& t) const {
+        lds_char* st = smem + stage * C::STAGE_BYTES;
+        if constexpr (D < C::A_PW) {
+            const int blk = wave * C::A_PW + D;
+            constexpr int par = D & 1;
+            const uint32_t soff = (uint32_t)blk * (uint32_t)(C::RPB * p.lda * 2) + t.k0x2;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ra, (__attribute__((address_space(3))) void*)(st + blk * 1024), 16, (int)L.a[par], (int)soff, 0, 0);
+        } else {
+            const int blk = wave * C::B_PW + (D - C::A_PW);
+            constexpr int par = (D - C::A_PW) & 1;
+            const uint32_t soff = (uint32_t)blk * (uint32_t)(C::RPB * p.ldb * 2) + t.k0x2;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rb, (__attribute__((address_space(3))) void*)(st + C::A_BYTES + blk * 1024), 16, (int)L.b[par],
+                (int)soff, 0, 0);
+        }
+    }
+
+    template <bool FAST, int D0, int D1>
     __device__ __forceinline__ void issue_range(const GemmParams& p, const __amdgpu_buffer_rsrc_t& ra,
                                                 const __amdgpu_buffer_rsrc_t& rb, int stage,
                                                 const DmaLane& L, const DmaIt& t) const {
         if constexpr (D0 < D1) {
-            issue_one<D0>(p, ra, rb, stage, L, t);
-            issue_range<D0 + 1, D1>(p, ra, rb, stage, L, t);
+            if constexpr (FAST) issue_one_fast<D0>(p, ra, rb, stage, L, t);
+            else issue_one<D0>(p, ra, rb, stage, L, t);
+            issue_range<FAST, D0 + 1, D1>(p, ra, rb, stage, L, t);
         }
     }
 
@@ -431,7 +460,7 @@ struct Engine {
         const DmaLane L = dma_lane(p);
 #pragma unroll
         for (int s = 0; s < S - 1; ++s)
-            if (u.kb + s < u.ke) issue_range<0, C::LOADS>(p, ra, rb, s, L, dma_it(p, u.kb + s, true));
+            if (u.kb + s < u.ke) issue_range<false, 0, C::LOADS>(p, ra, rb, s, L, dma_it(p, u.kb + s, true));
     }
 
     // Fragment registers: A (activation rows) double-buffered across k-steps, B (weight rows)
@@ -499,7 +528,7 @@ struct Engine {
         }
     }
 
-    template <int CB, int MODE, bool DMA, int KSI, int Q>
+    template <bool FAST, int CB, int MODE, bool DMA, int KSI, int Q>
     __device__ __forceinline__ void slot(const GemmParams& p, f32x16 (&acc)[FN][FM], int cur, int nxt,
                                          const __amdgpu_buffer_rsrc_t& ra, const __amdgpu_buffer_rsrc_t& rb,
                                          int dma_stage, const DmaLane& L, const DmaIt& o, const Unit& nx) {
@@ -537,22 +566,22 @@ struct Engine {
         constexpr int g = KSI * NM + Q;  // this slot's share of the refill DMA
         if constexpr (DMA && g < DMA_SLOTS && (KSI + 1 < KS || Q < SYNC_Q)) {
             constexpr int t0 = g * C::LOADS / DMA_SLOTS, t1 = (g + 1) * C::LOADS / DMA_SLOTS;
-            issue_range<t0, t1>(p, ra, rb, dma_stage, L, o);
+            issue_range<FAST, t0, t1>(p, ra, rb, dma_stage, L, o);
         }
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    template <int CB, int MODE, bool DMA, int KSI, int Q>
+    template <bool FAST, int CB, int MODE, bool DMA, int KSI, int Q>
     __device__ __forceinline__ void slots(const GemmParams& p, f32x16 (&acc)[FN][FM], int cur, int nxt,
                                           const __amdgpu_buffer_rsrc_t& ra, const __amdgpu_buffer_rsrc_t& rb,
                                           int dma_stage, const DmaLane& L, const DmaIt& o, const Unit& nx) {
         if constexpr (Q < NM) {
-            slot<CB, MODE, DMA, KSI, Q>(p, acc, cur, nxt, ra, rb, dma_stage, L, o, nx);
-            slots<CB, MODE, DMA, KSI, Q + 1>(p, acc, cur, nxt, ra, rb, dma_stage, L, o, nx);
+            slot<FAST, CB, MODE, DMA, KSI, Q>(p, acc, cur, nxt, ra, rb, dma_stage, L, o, nx);
+            slots<FAST, CB, MODE, DMA, KSI, Q + 1>(p, acc, cur, nxt, ra, rb, dma_stage, L, o, nx);
         }
     }
 
-    template <bool LAST, int KSI>
+    template <bool FAST, bool LAST, int KSI>
     __device__ __forceinline__ void ksteps(const GemmParams& p, const Unit& nx,
                                            const __amdgpu_buffer_rsrc_t& ra,
                                            const __amdgpu_buffer_rsrc_t& rb, int cur, int dstage,
@@ -562,8 +591,8 @@ struct Engine {
             const int nxt = (cur + 1 == S) ? 0 : cur + 1;
             // the last iteration of a unit refills nothing (its DMA prologue for the next unit
             // is issued after the barrier of its last k-step)
-            slots<KSI & 1, MODE, !LAST, KSI, 0>(p, acc, cur, nxt, ra, rb, dstage, L, o, nx);
-            ksteps<LAST, KSI + 1>(p, nx, ra, rb, cur, dstage, L, o, acc);
+            slots<FAST, KSI & 1, MODE, !LAST, KSI, 0>(p, acc, cur, nxt, ra, rb, dstage, L, o, nx);
+            ksteps<FAST, LAST, KSI + 1>(p, nx, ra, rb, cur, dstage, L, o, acc);
         }
     }
 
@@ -573,6 +602,7 @@ struct Engine {
     // of it-1; past the end of the unit it issues the same DMA with out-of-range offsets
     // (zeros into the free stage), which keeps every stage wait a compile-time count.  The
     // last iteration starts the DMA prologue of `nx`, which then overlaps this unit's epilogue.
+    template <bool FASTK>
     __device__ __forceinline__ void mainloop(const GemmParams& p, const Unit& u, const Unit& nx,
                                              f32x16 (&acc)[FN][FM]) {
 #pragma unroll
@@ -587,15 +617,29 @@ struct Engine {
         barrier();
         read_a_range<0, 0, FM>(0, 0);
         read_b_range<0, FN>(0, 0);
-        int cur = 0;
-        for (int it = 0; it < n - 1; ++it) {
+        // In a FASTK kernel, iterations whose refill targets a full K-iteration of an interior
+        // tile take the fast DMA path; the K tail, the zero-fill past the unit and edge tiles
+        // take the checked one.  (A kernel without FASTK carries the checked loop alone: the
+        // second loop body would raise its scalar register pressure.)
+        int cur = 0, it = 0;
+        if constexpr (FASTK) {
+            const bool interior = (u.tm + 1) * C::BM <= p.m_valid && (u.tn + 1) * C::BN <= p.N;
+            const int fast_end = interior ? max(0, min(n, p.K / C::BK - u.kb) - (S - 1)) : 0;
+            for (; it < fast_end && it < n - 1; ++it) {
+                const DmaIt o = dma_it(p, u.kb + it + S - 1, true);
+                const int dstage = (cur == 0) ? S - 1 : cur - 1;
+                ksteps<true, false, 0>(p, nx, ra, rb, cur, dstage, L, o, acc);
+                cur = (cur + 1 == S) ? 0 : cur + 1;
+            }
+        }
+        for (; it < n - 1; ++it) {
             const int dkit = it + S - 1;
             const DmaIt o = dma_it(p, u.kb + dkit, dkit < n);
             const int dstage = (cur == 0) ? S - 1 : cur - 1;
-            ksteps<false, 0>(p, nx, ra, rb, cur, dstage, L, o, acc);
+            ksteps<false, false, 0>(p, nx, ra, rb, cur, dstage, L, o, acc);
             cur = (cur + 1 == S) ? 0 : cur + 1;
         }
-        ksteps<true, 0>(p, nx, ra, rb, cur, 0, L, DmaIt{0u, 0}, acc);
+        ksteps<false, true, 0>(p, nx, ra, rb, cur, 0, L, DmaIt{0u, 0}, acc);
     }
 
     // ---- epilogue through LDS --------------------------------------------------------------
@@ -769,7 +813,7 @@ struct Engine {
 // Persistent GEMM: every workgroup walks its units (whole tiles, then for Stream-K its split
 // iterations) with the DMA of the next unit overlapping the epilogue of the current one.
 // Split pieces that share a tile publish FP32 partials; ffn_sk_reduce_kernel finishes them.
-template <int DT, class C, int EPI, bool SK>
+template <int DT, class C, int EPI, bool SK, bool FASTK>
 __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
     // The activation epilogue stores from registers, where its VALU work overlaps the stores;
     // the plain cast stages through LDS, whose full-row stores drain faster when every
@@ -793,7 +837,7 @@ __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
     eng.prologue(p, u);
     while (true) {
         const Unit nx = walk.next(p);
-        eng.mainloop(p, u, nx, acc);
+        eng.template mainloop<FASTK>(p, u, nx, acc);
         if (SK && u.split >= 0)
             eng.store_partial(sk_slot(p, v, u.local, C::BM * C::BN), acc);
         else if constexpr (EPI_IN_REGS)

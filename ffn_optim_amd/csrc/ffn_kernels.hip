@@ -26,21 +26,32 @@ using Cfg = VariantCfg<FFN_VARIANT>::type;
 #define FFN_CAT(a, b, c, d) FFN_CAT_(a, b, c, d)
 #define FFN_LAUNCHER FFN_CAT(ffn_launch_d, FFN_DT, _v, FFN_VARIANT)
 
+namespace {
+// one launch of ffn_gemm_kernel with the DMA addressing the plan chose
+template <int EPI, bool SK>
+void launch_gemm(const ffn::GemmParams* p, dim3 g, dim3 b, hipStream_t stream) {
+    if (p->fast_dma)
+        hipLaunchKernelGGL((ffn::ffn_gemm_kernel<FFN_DT, Cfg, EPI, SK, true>), g, b, 0, stream, *p);
+    else
+        hipLaunchKernelGGL((ffn::ffn_gemm_kernel<FFN_DT, Cfg, EPI, SK, false>), g, b, 0, stream, *p);
+}
+}  // namespace
+
 extern "C" hipError_t FFN_LAUNCHER(int role, const ffn::GemmParams* p, int grid, hipStream_t stream) {
     using namespace ffn;
     const dim3 g(grid), b(Cfg::NT);
     switch (role) {
         case FFN_ROLE_UP_ERF:
-            hipLaunchKernelGGL((ffn_gemm_kernel<FFN_DT, Cfg, EPI_GELU_ERF, false>), g, b, 0, stream, *p);
+            launch_gemm<EPI_GELU_ERF, false>(p, g, b, stream);
             break;
         case FFN_ROLE_UP_RATIONAL:
-            hipLaunchKernelGGL((ffn_gemm_kernel<FFN_DT, Cfg, EPI_GELU_RATIONAL, false>), g, b, 0, stream, *p);
+            launch_gemm<EPI_GELU_RATIONAL, false>(p, g, b, stream);
             break;
         case FFN_ROLE_DOWN_BASIC:
-            hipLaunchKernelGGL((ffn_gemm_kernel<FFN_DT, Cfg, EPI_STORE, false>), g, b, 0, stream, *p);
+            launch_gemm<EPI_STORE, false>(p, g, b, stream);
             break;
         case FFN_ROLE_DOWN_STREAMK: {
-            hipLaunchKernelGGL((ffn_gemm_kernel<FFN_DT, Cfg, EPI_STORE, true>), g, b, 0, stream, *p);
+            launch_gemm<EPI_STORE, true>(p, g, b, stream);
             if (p->sk_tiles > 0) {
                 // one reduce workgroup per accumulator group of each split tile: every partial
                 // load of the fixup is then in flight at once (a workgroup walking several
