@@ -513,11 +513,21 @@ struct Engine {
     static constexpr int SYNC_Q = C::SYNCQ >= 0 ? C::SYNCQ : FM - 1;
     static_assert(SYNC_Q >= FM - 1 && SYNC_Q < NM, "the barrier may not precede the in-place B reloads");
     // Slots carrying the refill DMA.  With two stages the data is waited for at the end of the
-    // same iteration, so it goes out in the first half; with more, it is spread over every slot
-    // before the stage wait (whose count assumes whole groups issued).
-    static constexpr int DMA_SLOTS = (S == 2) ? (C::DMAKS > 0 ? C::DMAKS : KS / 2) * NM
-                                              : (KS - 1) * NM + SYNC_Q;
+    // same iteration, so it goes out in the first half.  With more, it is spread over every
+    // slot before the stage wait, or (DMAKS == KS) over every slot of the iteration: the
+    // stage wait then also allows the part of this iteration's group issued after it.
+    static constexpr bool DMA_ALL = S > 2 && C::DMAKS == KS;
+    static constexpr int DMA_SLOTS = (S == 2)  ? (C::DMAKS > 0 ? C::DMAKS : KS / 2) * NM
+                                     : DMA_ALL ? KS * NM
+                                               : (KS - 1) * NM + SYNC_Q;
     static_assert(KS >= 2 && DMA_SLOTS >= 1, "at least two k-steps per stage");
+    // loads of the current iteration's group issued before the stage wait (after the MFMA and
+    // before the DMA of slot SYNC_Q of the last k-step)
+    static constexpr int DMA_BEFORE_WAIT =
+        DMA_ALL ? ((KS - 1) * NM + SYNC_Q) * C::LOADS / DMA_SLOTS : C::LOADS;
+    // outstanding loads allowed at the stage wait: the groups of the S-3 iterations after the
+    // one that fetched the next stage, plus this iteration's share so far
+    static constexpr int STAGE_WAIT = C::LOADS * (S - 3) + DMA_BEFORE_WAIT;
 
     template <int Q, int JJ>
     __device__ __forceinline__ void reload_b_at(int stage) {
@@ -547,7 +557,7 @@ struct Engine {
                 if constexpr (MODE == 1) {
                     // every wave's DMA of the next stage has landed; every wave is done with the
                     // stage the next refill overwrites
-                    wait_vmcnt<C::LOADS * (S - 2)>();
+                    wait_vmcnt<(S == 2 ? 0 : STAGE_WAIT)>();
                     barrier();
                 } else if (nx.valid) {
                     barrier();
@@ -564,7 +574,7 @@ struct Engine {
             }
         }
         constexpr int g = KSI * NM + Q;  // this slot's share of the refill DMA
-        if constexpr (DMA && g < DMA_SLOTS && (KSI + 1 < KS || Q < SYNC_Q)) {
+        if constexpr (DMA && g < DMA_SLOTS && (DMA_ALL || KSI + 1 < KS || Q < SYNC_Q)) {
             constexpr int t0 = g * C::LOADS / DMA_SLOTS, t1 = (g + 1) * C::LOADS / DMA_SLOTS;
             issue_range<FAST, t0, t1>(p, ra, rb, dma_stage, L, o);
         }

@@ -1,6 +1,8 @@
 // ffn_variants.hpp -- the macro-tile variants compiled into libffn_mi355x.so.
 //
 // X(id, BM, BN, BK, waves along M, waves along N, LDS stages[, sync slot, DMA k-steps])
+// (DMA k-steps equal to the k-steps per stage spreads a deep pipeline's refill over the
+// whole iteration.)
 // The deep-pipeline 64-row tiles (8, 9) keep 56 KiB or more of weights in flight per CU for
 // the memory-bound small-M (decode) shapes.
 // Each variant is built for both storage types and four epilogues (GELU-erf,
@@ -14,8 +16,8 @@
     X(3, 128, 128, 64, 2, 2, 2)         \
     X(4, 64, 64, 64, 2, 2, 2)           \
     X(5, 64, 128, 64, 2, 2, 3)          \
-    X(6, 256, 256, 32, 2, 2, 4)         \
-    X(7, 256, 256, 32, 2, 2, 5)         \
+    X(6, 256, 256, 32, 2, 2, 4, -1, 2)  \
+    X(7, 256, 256, 32, 2, 2, 5, -1, 2)  \
     X(8, 64, 64, 64, 2, 2, 8)           \
     X(9, 64, 128, 64, 2, 2, 6)
 
