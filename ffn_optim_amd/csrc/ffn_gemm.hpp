@@ -859,14 +859,16 @@ __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
     }
 }
 
-// Stream-K fixup, stream-ordered after ffn_gemm_kernel<..., true>: workgroup (s, r) sums the
-// FP32 partials of split tile s in ascending K order (independent of which workgroup finished
-// first), rounds once to the storage type and stores.  r selects a slice of the tile.
+// Stream-K fixup, stream-ordered after ffn_gemm_kernel<..., true>: workgroup (s, b) sums the
+// FP32 partials of 32x32 accumulator block b (of every wave) of split tile s in ascending K
+// order (independent of which workgroup finished first), rounds once to the storage type and
+// stores.  Each thread keeps the four 16-byte groups of its block in flight per piece, and the
+// same lane pairing as the GEMM's register epilogue (v_permlane32_swap) turns its output into
+// two 16-byte row segments.
 template <int DT, class C>
-__global__ void __launch_bounds__(C::NT) ffn_sk_reduce_kernel(GemmParams p, int slices) {
+__global__ void __launch_bounds__(C::NT) ffn_sk_reduce_kernel(GemmParams p, int blocks) {
     constexpr int TE = C::BM * C::BN;
-    constexpr int GROUPS = C::FN * C::FM * 4;
-    const int s = blockIdx.x / slices, r = blockIdx.x - s * slices;
+    const int s = blockIdx.x / blocks, ji = blockIdx.x - s * blocks;
     const int kI = p.k_iters;
     const int first = sk_owner(p, s * kI), last = sk_owner(p, s * kI + kI - 1);
     if (first == last) return;  // stored whole by its only contributor
@@ -874,21 +876,30 @@ __global__ void __launch_bounds__(C::NT) ffn_sk_reduce_kernel(GemmParams p, int 
     tile_coords(p, p.dp_tiles + s, tm, tn);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave % C::WGM, wn = wave / C::WGM;
-    const int per = (GROUPS + slices - 1) / slices;
-    const int g0 = r * per, g1 = min(GROUPS, g0 + per);
-    for (int idx = g0; idx < g1; ++idx) {
-        const int q = idx & 3, ji = idx >> 2;
-        const int j = ji / C::FM, i = ji - j * C::FM;
-        const size_t off = ((size_t)idx * C::NT + tid) * 4;
-        f32x4 tot = *(const f32x4*)(sk_slot(p, first, s - sk_start(p, first) / kI, TE) + off);
-        for (int w = first + 1; w <= last; ++w)
-            tot += *(const f32x4*)(sk_slot(p, w, s - sk_start(p, w) / kI, TE) + off);
-        const int m = tm * C::BM + wm * C::WTM + 32 * i + (lane & 31);
-        const int n = tn * C::BN + wn * C::WTN + 32 * j + 8 * q + 4 * (lane >> 5);
-        if (m < p.M && n < p.N) {
-            const u32x2 v = pack4<DT>(tot.x, tot.y, tot.z, tot.w);
-            *(u32x2*)((char*)p.c + ((size_t)m * (size_t)p.ldc + (size_t)n) * 2) = v;
-        }
+    const int j = ji / C::FM, i = ji - j * C::FM;
+    f32x4 tot[4];
+    {
+        const float* slot = sk_slot(p, first, s - sk_start(p, first) / kI, TE);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) tot[q] = *(const f32x4*)(slot + ((size_t)(ji * 4 + q) * C::NT + tid) * 4);
+    }
+    for (int w = first + 1; w <= last; ++w) {
+        const float* slot = sk_slot(p, w, s - sk_start(p, w) / kI, TE);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) tot[q] += *(const f32x4*)(slot + ((size_t)(ji * 4 + q) * C::NT + tid) * 4);
+    }
+    u32x2 g[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) g[q] = pack4<DT>(tot[q].x, tot[q].y, tot[q].z, tot[q].w);
+    const int m = tm * C::BM + wm * C::WTM + 32 * i + (lane & 31);
+    const int n0 = tn * C::BN + wn * C::WTN + 32 * j + 8 * (lane >> 5);
+#pragma unroll
+    for (int pp = 0; pp < 2; ++pp) {
+        const auto s0 = __builtin_amdgcn_permlane32_swap(g[2 * pp].x, g[2 * pp + 1].x, false, false);
+        const auto s1 = __builtin_amdgcn_permlane32_swap(g[2 * pp].y, g[2 * pp + 1].y, false, false);
+        const u32x4 v = {(uint32_t)s0[0], (uint32_t)s1[0], (uint32_t)s0[1], (uint32_t)s1[1]};
+        const int n = n0 + 16 * pp;
+        if (m < p.M && n < p.N) *(u32x4*)((char*)p.c + ((size_t)m * (size_t)p.ldc + (size_t)n) * 2) = v;
     }
 }
 

@@ -53,12 +53,12 @@ extern "C" hipError_t FFN_LAUNCHER(int role, const ffn::GemmParams* p, int grid,
         case FFN_ROLE_DOWN_STREAMK: {
             launch_gemm<EPI_STORE, true>(p, g, b, stream);
             if (p->sk_tiles > 0) {
-                // one reduce workgroup per accumulator group of each split tile: every partial
-                // load of the fixup is then in flight at once (a workgroup walking several
-                // groups serialises their memory latencies)
-                constexpr int groups = Cfg::FN * Cfg::FM * 4;
-                hipLaunchKernelGGL((ffn_sk_reduce_kernel<FFN_DT, Cfg>), dim3(p->sk_tiles * groups), b, 0,
-                                   stream, *p, groups);
+                // one reduce workgroup per 32x32 accumulator block of each split tile: every
+                // partial load of the fixup is then in flight at once (a workgroup walking
+                // several blocks serialises their memory latencies)
+                constexpr int blocks = Cfg::FN * Cfg::FM;
+                hipLaunchKernelGGL((ffn_sk_reduce_kernel<FFN_DT, Cfg>), dim3(p->sk_tiles * blocks), b, 0,
+                                   stream, *p, blocks);
             }
             break;
         }
