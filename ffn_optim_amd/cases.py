@@ -16,7 +16,7 @@ from pathlib import Path
 from .host.inputs import problem_from_shapes
 
 CONFIGS = Path(__file__).resolve().parent / "configs"
-BASELINE_CASES = CONFIGS / "baseline_cases.json"
+BENCH_CASES = CONFIGS / "benchmark_cases.json"
 V1_CASES = CONFIGS / "v1_cases.json"
 X_VIEWS = (None, "transpose12")
 
@@ -53,7 +53,7 @@ def case_problem(case):
 
 
 def get_case(case_id, path=None):
-    for path in ([path] if path else [BASELINE_CASES, V1_CASES]):
+    for path in ([path] if path else [BENCH_CASES, V1_CASES]):
         for case in load_cases(path):
             if case["case_id"] == case_id:
                 return case

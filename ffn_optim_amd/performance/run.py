@@ -6,7 +6,7 @@ against the FP32 golden, event timing and (with --profile) a separate profiler p
 
     python -m ffn_optim_amd.performance.run --mode search --execute-gpu
     python -m ffn_optim_amd.performance.run --mode tune --execute-gpu --write-tuned \\
-        --cases ffn_optim_amd/configs/baseline_cases.json
+        --cases ffn_optim_amd/configs/benchmark_cases.json
 
 Every run creates results/<run_id>/ with manifest.json, accuracy.json,
 performance.csv, best_configs.json, analysis.md and profiler/; earlier runs are

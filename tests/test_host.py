@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from ffn_optim_amd import _lib
-from ffn_optim_amd.cases import (BASELINE_CASES, V1_CASES, case_problem, load_cases,
+from ffn_optim_amd.cases import (BENCH_CASES, V1_CASES, case_problem, load_cases,
                                  make_inputs)
 from ffn_optim_amd.host.dispatch import (DependencyUnavailable, NotApplicable, Selection,
                                          verify_dependency)
@@ -100,9 +100,9 @@ def test_selection():
     assert make_plan(p, Selection(), 8).workspace_shape == (1, 1)
 
 
-def test_baseline_cases_plan_for_both_down_impls():
+def test_benchmark_cases_plan_for_both_down_impls():
     """Every measured workload is plannable for Basic and Stream-K at 256 workgroups."""
-    for case in load_cases(BASELINE_CASES):
+    for case in load_cases(BENCH_CASES):
         p = case_problem(case)
         for down in ("basic", "streamk"):
             plan = make_plan(p, Selection(down_impl=down), 256)
@@ -168,7 +168,7 @@ def test_c_abi_error_codes_without_gpu():
 
 def test_make_inputs_contract():
     """common/cases.py:34-50: deterministic, scaled by fan-in, stride-2 and transposed views."""
-    for case in load_cases(BASELINE_CASES)[:1] + load_cases(V1_CASES):
+    for case in load_cases(BENCH_CASES)[:1] + load_cases(V1_CASES):
         x, w1, w2 = make_inputs(case)
         x2, _, _ = make_inputs(case)
         assert torch.equal(x, x2)
@@ -176,12 +176,12 @@ def test_make_inputs_contract():
         assert tuple(x.shape) == p.input_shape and w1.shape == (p.h, p.k) and w2.shape == (p.n, p.h)
         if case.get("noncontiguous"):
             assert x.stride()[-1] == 2 and w1.stride()[-1] == 2
-    case = load_cases(BASELINE_CASES)[0]
+    case = load_cases(BENCH_CASES)[0]
     x, w1, w2 = make_inputs(case)
     assert abs(x.float().std().item() - 1.0) < 0.02
     assert abs(w1.float().std().item() * 256 ** 0.5 - 1.0) < 0.02
     assert abs(w2.float().std().item() * 1024 ** 0.5 - 1.0) < 0.02
-    t = dict(load_cases(BASELINE_CASES)[2], shape=[3, 5, 7, 8], weight1_shape=[9, 8],
+    t = dict(load_cases(BENCH_CASES)[2], shape=[3, 5, 7, 8], weight1_shape=[9, 8],
              weight2_shape=[4, 9])
     xt, _, _ = make_inputs(t)
     xc, _, _ = make_inputs(dict(t, x_view=None))
