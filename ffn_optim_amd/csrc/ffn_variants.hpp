@@ -18,7 +18,7 @@
     X(5, 64, 128, 64, 2, 2, 3)          \
     X(6, 256, 256, 32, 2, 2, 4, -1, 2)  \
     X(7, 256, 256, 32, 2, 2, 5, -1, 2)  \
-    X(8, 64, 64, 64, 2, 2, 8)           \
+    X(8, 64, 64, 64, 2, 2, 8, -1, 4)    \
     X(9, 64, 128, 64, 2, 2, 6)
 
 #define FFN_NUM_VARIANTS 10
