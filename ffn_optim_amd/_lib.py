@@ -27,7 +27,8 @@ class PlanStruct(ctypes.Structure):
         "up_variant", "down_variant", "up_bm", "up_bn", "up_bk",
         "down_bm", "down_bn", "down_bk", "up_tiles", "up_grid",
         "down_tiles", "down_grid", "down_k_iters", "down_dp_tiles",
-        "down_sk_tiles", "down_slots_per_wg")] + [("workspace_bytes", ctypes.c_size_t)]
+        "down_sk_tiles", "down_slots_per_wg")] + [("workspace_bytes", ctypes.c_size_t)] + [
+        (name, ctypes.c_int) for name in ("k", "h", "n", "ldx", "ldw1", "ldw2")]
 
     def to_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}
@@ -40,6 +41,7 @@ SIGNATURES = {
     "ffn_mi355x_query": (_i, [_i, _P(_i), ctypes.c_char_p, _i]),
     "ffn_mi355x_make_plan": (_i, [_i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _P(PlanStruct)]),
     "ffn_mi355x_workspace_bytes": (_i, [_P(PlanStruct), _P(ctypes.c_size_t)]),
+    "ffn_mi355x_set_operands": (_i, [_P(PlanStruct), _i, _i, _i, _i, _i, _i]),
     "ffn_mi355x_run": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ffn_mi355x_up": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp]),
     "ffn_mi355x_down": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp]),
@@ -113,6 +115,11 @@ def make_plan(mp, kp, hp, np_, dtype, down_impl, gelu, block_num, up_variant=-1,
                                       GELU_CODES[gelu], block_num, up_variant, down_variant,
                                       ctypes.byref(plan)))
     return plan
+
+
+def set_operands(plan: PlanStruct, k, h, n, ldx, ldw1, ldw2) -> None:
+    """Point a native plan at operands of their logical widths (ffn_mi355x_set_operands)."""
+    check(load().ffn_mi355x_set_operands(ctypes.byref(plan), k, h, n, ldx, ldw1, ldw2))
 
 
 def variants() -> list[dict]:

@@ -34,7 +34,7 @@ class PreparedFFN:
     """Prepared inputs, buffers and bound kernels; run() may be called repeatedly.
 
     storage is (X[mp,kp], W1[hp,kp], W2[np,hp], hidden[mp,hp], out[mp,np], ws) on
-    one device; tensors holds their device addresses; provenance and preparation
+    one device (for ffn(), operands read in place keep their own shapes); tensors holds their device addresses; provenance and preparation
     record the library and the preparation timings; stream is the preparation
     stream (ops/api.py:17-35).
     """
@@ -94,8 +94,9 @@ def prepare_ffn(x, weight1, weight2, *, up_impl="basic", down_impl="basic", bloc
         stream = torch.cuda.current_stream()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
-        storage = prepare_storage(x, weight1, weight2, plan, alias_aligned=_alias)
+        storage, layout = prepare_storage(x, weight1, weight2, plan, alias_aligned=_alias)
         end.record()
+        _lib.set_operands(plan.native, *layout)
         end.synchronize()
         auxiliary_ms = start.elapsed_time(end)
         tensors = tuple(t.data_ptr() for t in storage)
@@ -112,8 +113,9 @@ def prepare_ffn(x, weight1, weight2, *, up_impl="basic", down_impl="basic", bloc
 def ffn(x, weight1, weight2, **configuration):
     """Y = GELU(X @ weight1.T) @ weight2.T; no bias, no autograd (ops/api.py:92-94).
 
-    Operands that are contiguous with K, H and N already multiples of 16/64/64 are used
-    in place for this single launch instead of being copied into padded buffers; the
-    result is identical (the kernels read no padding rows and mask ragged tiles).
+    Operands the kernels can read where they lie (contiguous, rows a multiple of 8
+    elements: K for X and weight1, H for weight2) are used in place for this single
+    launch instead of being copied into padded buffers; the result is identical (the
+    kernels zero-fill past the logical widths and mask ragged tiles).
     """
     return prepare_ffn(x, weight1, weight2, **configuration, _alias=True).run()

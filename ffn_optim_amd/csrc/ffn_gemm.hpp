@@ -49,6 +49,7 @@ struct GemmParams {
     float* ws;            // Stream-K partial-tile slots (FP32)
     int M, N, K;
     int m_valid;          // rows of A holding data; rows [m_valid, M) are zero padding
+    int n_valid;          // rows of B holding data; rows [n_valid, N) read as zero
     int lda, ldb, ldc;
     int tiles_m, tiles_n;
     int k_iters;          // ceil(K / BK)
@@ -345,7 +346,7 @@ struct Engine {
         const char* bbase = (const char*)p.b + (size_t)col0 * (size_t)ldb2;
         // zero-padding rows of A are not fetched: past m_valid the range check returns zeros
         ra = make_rsrc(abase, (uint32_t)max(0, min(C::BM, p.m_valid - row0)) * (uint32_t)lda2);
-        rb = make_rsrc(bbase, (uint32_t)min(C::BN, p.N - col0) * (uint32_t)ldb2);
+        rb = make_rsrc(bbase, (uint32_t)max(0, min(C::BN, p.n_valid - col0)) * (uint32_t)ldb2);
     }
 
     // Per-lane DMA addressing, computed once per unit.  The lane fills physical chunk pc of
@@ -633,7 +634,7 @@ struct Engine {
         // second loop body would raise its scalar register pressure.)
         int cur = 0, it = 0;
         if constexpr (FASTK) {
-            const bool interior = (u.tm + 1) * C::BM <= p.m_valid && (u.tn + 1) * C::BN <= p.N;
+            const bool interior = (u.tm + 1) * C::BM <= p.m_valid && (u.tn + 1) * C::BN <= p.n_valid;
             const int fast_end = interior ? max(0, min(n, p.K / C::BK - u.kb) - (S - 1)) : 0;
             for (; it < fast_end && it < n - 1; ++it) {
                 const DmaIt o = dma_it(p, u.kb + it + S - 1, true);

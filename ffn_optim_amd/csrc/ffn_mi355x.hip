@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <climits>
+#include <cstdint>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -183,8 +184,20 @@ int group_m_for(long long tiles_m) { return (int)(tiles_m < 8 ? tiles_m : 8); }
 constexpr int kFastDmaMaxK = 8192;
 int fast_dma_for(int k) { return k <= kFastDmaMaxK ? 1 : 0; }
 
+// Depth of the down GEMM's reduction: the logical H when hidden rows can be read to it in
+// whole 16-byte chunks, else the padded H (W2 then spans hp columns, zero past h).
+int down_depth(const ffn_mi355x_plan* p) { return p->h % 8 == 0 ? p->h : p->hp; }
+
+bool layout_ok(const ffn_mi355x_plan* p) {
+    return p->k >= 1 && p->k <= p->kp && (p->k % 8 == 0 || p->k == p->kp) && p->h >= 1 && p->h <= p->hp &&
+           p->n >= 1 && p->n <= p->np && p->ldx >= p->k && p->ldx % 8 == 0 && p->ldw1 >= p->k &&
+           p->ldw1 % 8 == 0 && p->ldw2 >= down_depth(p) && p->ldw2 % 8 == 0;
+}
+
+bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+
 bool valid_plan(const ffn_mi355x_plan* p) {
-    return p && p->m >= 1 && p->m <= p->mp && p->up_variant >= 0 && p->up_variant < kNumVariants && p->down_variant >= 0 &&
+    return p && p->m >= 1 && p->m <= p->mp && layout_ok(p) && p->up_variant >= 0 && p->up_variant < kNumVariants && p->down_variant >= 0 &&
            p->down_variant < kNumVariants && (p->dtype == 0 || p->dtype == 1) &&
            (p->down_impl == FFN_MI355X_DOWN_BASIC || p->down_impl == FFN_MI355X_DOWN_STREAMK) &&
            (p->gelu == 0 || p->gelu == 1) && p->block_num >= 1;
@@ -304,8 +317,25 @@ int ffn_mi355x_make_plan(int m, int mp, int kp, int hp, int np, int dtype, int d
         plan->down_grid = plan->down_tiles < G ? plan->down_tiles : G;
         plan->workspace_bytes = 0;
     }
+    plan->k = kp, plan->h = hp, plan->n = np;
+    plan->ldx = kp, plan->ldw1 = kp, plan->ldw2 = hp;
     return ok();
 }
+
+int ffn_mi355x_set_operands(ffn_mi355x_plan* plan, int k, int h, int n, int ldx, int ldw1, int ldw2) {
+    if (!plan) return fail(FFN_MI355X_EINVAL, "plan must not be NULL");
+    ffn_mi355x_plan t = *plan;
+    t.k = k, t.h = h, t.n = n, t.ldx = ldx, t.ldw1 = ldw1, t.ldw2 = ldw2;
+    if (!layout_ok(&t))
+        return fail(FFN_MI355X_EINVAL,
+                    "operand layout k=%d h=%d n=%d ldx=%d ldw1=%d ldw2=%d does not fit the plan "
+                    "(kp=%d hp=%d np=%d): k a multiple of 8 or kp, pitches multiples of 8 covering "
+                    "the widths, W2 spanning hp columns when h is not a multiple of 8",
+                    k, h, n, ldx, ldw1, ldw2, plan->kp, plan->hp, plan->np);
+    *plan = t;
+    return ok();
+}
+
 
 int ffn_mi355x_workspace_bytes(const ffn_mi355x_plan* plan, size_t* bytes) {
     if (!plan || !bytes) return fail(FFN_MI355X_EINVAL, "NULL argument");
@@ -317,13 +347,16 @@ int ffn_mi355x_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, vo
                   void* hip_stream) {
     if (!valid_plan(plan)) return fail(FFN_MI355X_EINVAL, "invalid plan");
     if (!x || !w1 || !hidden) return fail(FFN_MI355X_EINVAL, "NULL device buffer");
+    if (!aligned16(x) || !aligned16(w1) || !aligned16(hidden))
+        return fail(FFN_MI355X_EINVAL, "device buffers must be 16-byte aligned");
     const Variant& U = kVariants[plan->up_variant];
     ffn::GemmParams gp;
     memset(&gp, 0, sizeof gp);
     gp.a = x, gp.b = w1, gp.c = hidden;
-    gp.M = plan->mp, gp.N = plan->hp, gp.K = plan->kp;
-    gp.m_valid = plan->m;
-    gp.lda = plan->kp, gp.ldb = plan->kp, gp.ldc = plan->hp;
+    // all hp hidden columns are written: those past h from zero rows of W1, GELU(0) = 0
+    gp.M = plan->mp, gp.N = plan->hp, gp.K = plan->k;
+    gp.m_valid = plan->m, gp.n_valid = plan->h;
+    gp.lda = plan->ldx, gp.ldb = plan->ldw1, gp.ldc = plan->hp;
     gp.tiles_m = (int)cdiv(plan->mp, U.bm), gp.tiles_n = (int)cdiv(plan->hp, U.bn);
     gp.k_iters = (int)cdiv(plan->kp, U.bk);
     gp.dp_tiles = gp.tiles_m * gp.tiles_n;
@@ -337,13 +370,15 @@ int ffn_mi355x_down(const ffn_mi355x_plan* plan, const void* hidden, const void*
                     void* ws, void* hip_stream) {
     if (!valid_plan(plan)) return fail(FFN_MI355X_EINVAL, "invalid plan");
     if (!hidden || !w2 || !out) return fail(FFN_MI355X_EINVAL, "NULL device buffer");
+    if (!aligned16(hidden) || !aligned16(w2) || !aligned16(out) || (ws && !aligned16(ws)))
+        return fail(FFN_MI355X_EINVAL, "device buffers must be 16-byte aligned");
     const Variant& D = kVariants[plan->down_variant];
     ffn::GemmParams gp;
     memset(&gp, 0, sizeof gp);
     gp.a = hidden, gp.b = w2, gp.c = out;
-    gp.M = plan->mp, gp.N = plan->np, gp.K = plan->hp;
-    gp.m_valid = plan->m;
-    gp.lda = plan->hp, gp.ldb = plan->hp, gp.ldc = plan->np;
+    gp.M = plan->mp, gp.N = plan->np, gp.K = down_depth(plan);
+    gp.m_valid = plan->m, gp.n_valid = plan->n;
+    gp.lda = plan->hp, gp.ldb = plan->ldw2, gp.ldc = plan->np;
     gp.tiles_m = (int)cdiv(plan->mp, D.bm), gp.tiles_n = (int)cdiv(plan->np, D.bn);
     gp.k_iters = plan->down_k_iters;
     gp.group_m = group_m_for(gp.tiles_m);

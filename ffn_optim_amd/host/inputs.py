@@ -83,9 +83,16 @@ def validate_tensors(x, weight1, weight2, layout="linear", require_device=False)
                                str(x.dtype).removeprefix("torch."), layout)
 
 
+def _in_place(t, width):
+    """A [rows, width] operand the kernels can read where it lies: contiguous rows of a
+    multiple of 8 elements on a 16-byte boundary (whole 16-byte chunks per row)."""
+    return t.is_contiguous() and width % 8 == 0 and t.data_ptr() % 16 == 0
+
+
 def operands_aligned(x, weight1, weight2, plan):
-    """True when X, W1 and W2 can be used in place: contiguous, K, H and N already at their
-    padded widths.  M needs no padding: the kernels never read rows of X past m."""
+    """True when X, W1 and W2 can all be used in place at the padded widths: contiguous, K,
+    H and N already at their padded extents.  M needs no padding: the kernels never read
+    rows of X past m."""
     p = plan.problem
     return (p.k == plan.kp and p.h == plan.hp and p.n == plan.np and x.is_contiguous()
             and weight1.is_contiguous() and weight2.is_contiguous())
@@ -95,27 +102,42 @@ def prepare_storage(x, weight1, weight2, plan, alias_aligned=False):
     """Contiguise and zero-pad into [mp,kp], [hp,kp], [np,hp]; allocate hidden, out, workspace.
 
     Same buffers as ops/host/inputs.py:74-90; the FP32 workspace holds the Stream-K
-    partial tiles (every slot is written before it is read).  With alias_aligned and
-    operands_aligned(), X ([m,kp] view), W1 and W2 are the caller's tensors themselves,
-    not copies: for a launch that runs before the caller can modify them.
+    partial tiles (every slot is written before it is read).  Returns the six buffers and
+    the operand layout (k, h, n, ldx, ldw1, ldw2) for ffn_mi355x_set_operands.
+
+    With alias_aligned, every operand the kernels can read where it lies (_in_place) is
+    the caller's tensor itself, at its logical width, and only the others are copied:
+    for a launch that runs before the caller can modify them.  X needs K % 8 == 0, W1 the
+    same, W2 H % 8 == 0; a non-contiguous operand (a transposed view) is always copied.
     """
     import torch
 
     p = plan.problem
-    if alias_aligned and operands_aligned(x, weight1, weight2, plan):
-        hidden = torch.empty((plan.mp, plan.hp), device=x.device, dtype=x.dtype)
-        out = torch.empty((plan.mp, plan.np), device=x.device, dtype=x.dtype)
-        ws = torch.empty(plan.workspace_shape, device=x.device, dtype=torch.float32)
-        return x.view(p.m, p.k), weight1, weight2, hidden, out, ws
-    xc = x.contiguous().view(p.m, p.k)
-    w1c, w2c = weight1.contiguous(), weight2.contiguous()
-    xp = torch.zeros((plan.mp, plan.kp), device=x.device, dtype=x.dtype)
-    w1p = torch.zeros((plan.hp, plan.kp), device=x.device, dtype=x.dtype)
-    w2p = torch.zeros((plan.np, plan.hp), device=x.device, dtype=x.dtype)
-    xp[:p.m, :p.k].copy_(xc)
-    w1p[:p.h, :p.k].copy_(w1c)
-    w2p[:p.n, :p.h].copy_(w2c)
     hidden = torch.empty((plan.mp, plan.hp), device=x.device, dtype=x.dtype)
     out = torch.empty((plan.mp, plan.np), device=x.device, dtype=x.dtype)
     ws = torch.empty(plan.workspace_shape, device=x.device, dtype=torch.float32)
-    return xp, w1p, w2p, hidden, out, ws
+    xv = x.reshape(p.m, p.k) if x.is_contiguous() else None
+    if alias_aligned and xv is not None and _in_place(xv, p.k):
+        xs, ldx = xv, p.k
+    else:
+        xs = torch.zeros((plan.mp, plan.kp), device=x.device, dtype=x.dtype)
+        xs[:p.m, :p.k].copy_(x.reshape(p.m, p.k))
+        ldx = plan.kp
+    if alias_aligned and _in_place(weight1, p.k):
+        w1s, ldw1 = weight1, p.k
+    else:
+        w1s = torch.zeros((plan.hp, plan.kp), device=x.device, dtype=x.dtype)
+        w1s[:p.h, :p.k].copy_(weight1)
+        ldw1 = plan.kp
+    if alias_aligned and _in_place(weight2, p.h):
+        w2s, ldw2 = weight2, p.h
+    else:
+        w2s = torch.zeros((plan.np, plan.hp), device=x.device, dtype=x.dtype)
+        w2s[:p.n, :p.h].copy_(weight2)
+        ldw2 = plan.hp
+    # the reduction runs to the logical K when both up operands hold whole chunks up to it
+    k = p.k if p.k % 8 == 0 else plan.kp
+    layout = (k, p.h, p.n, ldx, ldw1, ldw2)
+    return (xs, w1s, w2s, hidden, out, ws), layout
+
+

@@ -63,6 +63,11 @@ typedef struct ffn_mi355x_plan {
     int down_sk_tiles;           /* tiles whose H-range is split over workgroups */
     int down_slots_per_wg;       /* FP32 partial-tile slots per workgroup */
     size_t workspace_bytes;      /* FP32 partial-tile slots of the Stream-K down */
+    /* Operand layout.  ffn_mi355x_make_plan sets the padded buffers (k = kp, h = hp,
+       n = np, ldx = ldw1 = kp, ldw2 = hp); ffn_mi355x_set_operands may point the plan at
+       operands of their logical widths instead. */
+    int k, h, n;                 /* logical K, H and N */
+    int ldx, ldw1, ldw2;         /* row pitches, in elements, of X, W1 and W2 */
 } ffn_mi355x_plan;
 
 /* Device check replacing the Ascend950/AIC checks of ops/api.py:58-66:
@@ -81,6 +86,16 @@ int ffn_mi355x_query(int device, int* cu_count, char* arch, int arch_len);
 int ffn_mi355x_make_plan(int m, int mp, int kp, int hp, int np, int dtype, int down_impl,
                          int gelu, int block_num, int up_variant, int down_variant,
                          ffn_mi355x_plan* plan);
+
+/* Reads the operands in place at their logical widths instead of from buffers padded
+ * to the plan's extents: X [m, k] with row pitch ldx, W1 [h, k] with pitch ldw1, W2 [n, h]
+ * with pitch ldw2 (elements; each row 16-byte aligned, i.e. pitches and the base addresses
+ * multiples of 8 elements / 16 bytes).  Columns past k and rows past h and n read as zero
+ * through the kernels' range checks, and hidden columns [h, hp) are written as GELU(0) = 0.
+ * k must be a multiple of 8 or equal kp; with h not a multiple of 8, W2 must span hp
+ * columns (ldw2 >= hp, zero past h).  No counterpart in the reference, whose prepare step
+ * always copies into padded buffers (ops/host/inputs.py:74-90).  EINVAL on a bad layout. */
+int ffn_mi355x_set_operands(ffn_mi355x_plan* plan, int k, int h, int n, int ldx, int ldw1, int ldw2);
 
 /* Workspace bytes a plan needs (0 for the Basic down). */
 int ffn_mi355x_workspace_bytes(const ffn_mi355x_plan* plan, size_t* bytes);

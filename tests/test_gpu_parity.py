@@ -253,10 +253,12 @@ def test_harness_manual_run_on_device(tmp_path):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("shape", [((4, 25, 128), 256, 64), ((300, 1024), 512, 192), ((3, 37, 120), 200, 72)])
+@pytest.mark.parametrize("shape", [((4, 25, 128), 256, 64), ((300, 1024), 512, 192), ((3, 37, 120), 200, 72),
+                                   ((5, 201, 1000), 3001, 999), ((70, 100), 136, 40)])
 def test_one_shot_ffn_in_place_matches_prepared(shape):
-    """ffn() on aligned inputs skips the padded copies; results are bit-identical to the
-    prepared (copied) path, and PreparedFFN keeps its snapshot of the inputs."""
+    """ffn() reads operands in place where their rows allow it (at their logical widths:
+    K=120 and H=200 unpadded, C3-like H=3001 with W2 copied, K=100 copied); results are
+    bit-identical to the prepared (copied) path, and PreparedFFN keeps its snapshot."""
     from ffn_optim_amd import ffn
     xs, h, n = shape
     k = xs[-1]

@@ -31,7 +31,8 @@ def test_ranks_and_padding():
             w2 = torch.randn(23, 38).to(dtype)[:, ::2]
             p = validate_tensors(x, w1, w2)
             plan = make_plan(p)
-            xp, a, b, hidden, out, ws = prepare_storage(x, w1, w2, plan)
+            (xp, a, b, hidden, out, ws), layout = prepare_storage(x, w1, w2, plan)
+            assert layout == (p.k if p.k % 8 == 0 else plan.kp, p.h, p.n, plan.kp, plan.kp, plan.hp)
             assert xp.shape == (plan.mp, plan.kp) and a.shape == (plan.hp, plan.kp)
             assert b.shape == (plan.np, plan.hp) and hidden.shape == (plan.mp, plan.hp)
             assert out.shape == (plan.mp, plan.np) and ws.dtype == torch.float32
@@ -198,29 +199,63 @@ def test_case_schema_rejects_bad_files(tmp_path):
             load_cases(bad)
 
 
-def test_aligned_operands_used_in_place_only_when_asked():
+def test_operands_used_in_place_only_when_asked():
     import torch
     from ffn_optim_amd.host.dispatch import Selection
     from ffn_optim_amd.host.inputs import operands_aligned, prepare_storage, problem_from_shapes
     from ffn_optim_amd.host.tiling import make_plan
     g = torch.Generator().manual_seed(0)
-    # aligned K/H/N, ragged M (m=100): X is used as [m, kp] in place
+    # aligned K/H/N, ragged M (m=100): X is used as [m, k] in place
     x = torch.randn(4, 25, 128, generator=g).half()
     w1, w2 = torch.randn(256, 128, generator=g).half(), torch.randn(64, 256, generator=g).half()
     plan = make_plan(problem_from_shapes(x.shape, w1.shape, w2.shape, "float16"), Selection(), 8)
     assert operands_aligned(x, w1, w2, plan)
-    xs, w1s, w2s, hid, out, ws = prepare_storage(x, w1, w2, plan, alias_aligned=True)
+    (xs, w1s, w2s, hid, out, ws), layout = prepare_storage(x, w1, w2, plan, alias_aligned=True)
     assert xs.data_ptr() == x.data_ptr() and xs.shape == (100, 128)
-    assert w1s is w1 and w2s is w2
+    assert w1s is w1 and w2s is w2 and layout == (128, 256, 64, 128, 128, 256)
     assert hid.shape == (128, 256) and out.shape == (128, 64)
     # without the request the storage is a padded snapshot
-    xs, w1s, _, _, _, _ = prepare_storage(x, w1, w2, plan)
+    (xs, w1s, _, _, _, _), layout = prepare_storage(x, w1, w2, plan)
     assert xs.data_ptr() != x.data_ptr() and xs.shape == (128, 128)
     assert torch.equal(xs[:100], x.view(100, 128)) and not xs[100:].any()
-    # unaligned K, or a non-contiguous X, is always copied and padded
-    for xx, ww1 in ((torch.randn(100, 120, generator=g).half(), torch.randn(256, 120, generator=g).half()),
+    assert layout == (128, 256, 64, plan.kp, plan.kp, plan.hp)
+    # widths below the padded extents but whole 16-byte rows: still in place, unpadded
+    x2 = torch.randn(37, 120, generator=g).half()
+    w12, w22 = torch.randn(200, 120, generator=g).half(), torch.randn(72, 200, generator=g).half()
+    p2 = make_plan(problem_from_shapes(x2.shape, w12.shape, w22.shape, "float16"), Selection(), 8)
+    assert not operands_aligned(x2, w12, w22, p2)
+    (xs, w1s, w2s, _, _, _), layout = prepare_storage(x2, w12, w22, p2, alias_aligned=True)
+    assert xs.data_ptr() == x2.data_ptr() and w1s is w12 and w2s is w22
+    assert layout == (120, 200, 72, 120, 120, 200)
+    # H not a multiple of 8: W2 is copied into [np, hp]; W1 [h, k] stays in place
+    w13, w23 = torch.randn(201, 120, generator=g).half(), torch.randn(72, 201, generator=g).half()
+    p3 = make_plan(problem_from_shapes(x2.shape, w13.shape, w23.shape, "float16"), Selection(), 8)
+    (xs, w1s, w2s, _, _, _), layout = prepare_storage(x2, w13, w23, p3, alias_aligned=True)
+    assert w1s is w13 and w2s.shape == (p3.np, p3.hp) and not w2s[:, 201:].any()
+    assert layout == (120, 201, 72, 120, 120, p3.hp)
+    # K not a multiple of 8, or a non-contiguous X: copied and padded
+    for xx, ww1 in ((torch.randn(100, 100, generator=g).half(), torch.randn(256, 100, generator=g).half()),
                     (x.transpose(0, 1), w1)):
         p = make_plan(problem_from_shapes(xx.shape, ww1.shape, w2.shape, "float16"), Selection(), 8)
-        assert not operands_aligned(xx, ww1, w2, p)
-        xs = prepare_storage(xx, ww1, w2, p, alias_aligned=True)[0]
+        (xs, w1s, _, _, _, _), layout = prepare_storage(xx, ww1, w2, p, alias_aligned=True)
         assert xs.data_ptr() != xx.data_ptr() and xs.shape == (p.mp, p.kp)
+        assert layout[3] == p.kp and (layout[0] == p.kp or xx.shape[-1] % 8 == 0)
+
+
+def test_set_operands_validates_layout():
+    """ffn_mi355x_set_operands accepts logical widths with 16-byte rows and rejects the rest
+    without touching the plan."""
+    from ffn_optim_amd import _lib
+    plan = _lib.make_plan(1024, 1008, 3008, 1024, _lib.FP16, "basic", "erf", 256, m=1005)
+    assert (plan.k, plan.h, plan.n, plan.ldx, plan.ldw1, plan.ldw2) == (1008, 3008, 1024, 1008, 1008, 3008)
+    _lib.set_operands(plan, 1000, 3001, 999, 1000, 1000, 3008)
+    assert (plan.k, plan.h, plan.n, plan.ldx, plan.ldw1, plan.ldw2) == (1000, 3001, 999, 1000, 1000, 3008)
+    for bad in ((1004, 3001, 999, 1008, 1008, 3008),   # K neither a multiple of 8 nor kp
+                (1000, 3001, 999, 996, 1000, 3008),    # pitch below K
+                (1000, 3001, 999, 1004, 1000, 3008),   # pitch not a multiple of 8
+                (1000, 3001, 999, 1000, 1000, 3001),   # H not a multiple of 8 and W2 short of hp
+                (1000, 3009, 999, 1000, 1000, 3016),   # H above hp
+                (1000, 3000, 1025, 1000, 1000, 3000)): # N above np
+        with pytest.raises(ValueError):
+            _lib.set_operands(plan, *bad)
+        assert (plan.k, plan.h, plan.n) == (1000, 3001, 999)
