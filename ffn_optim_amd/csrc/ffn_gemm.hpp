@@ -63,13 +63,16 @@ struct GemmParams {
 
 // SYNCQ_: MFMA slot of a stage's last k-step after which the stage wait + barrier is placed
 // (-1: end of the first block of B).  DMAKS_: k-steps of an iteration carrying the refill DMA
-// with two stages (-1: the first half).
-template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int STAGES_, int SYNCQ_ = -1, int DMAKS_ = -1>
+// with two stages (-1: the first half).  WGK_: waves along K -- each wave computes its whole
+// WTM x WTN wave tile over its own BK/WGK slice of every stage, and the WGK partial tiles are
+// summed through LDS after the main loop.
+template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int STAGES_, int SYNCQ_ = -1, int DMAKS_ = -1,
+          int WGK_ = 1>
 struct TileCfg {
     static constexpr int BM = BM_, BN = BN_, BK = BK_;
-    static constexpr int WGM = WGM_, WGN = WGN_, STAGES = STAGES_;
+    static constexpr int WGM = WGM_, WGN = WGN_, WGK = WGK_, STAGES = STAGES_;
     static constexpr int SYNCQ = SYNCQ_, DMAKS = DMAKS_;
-    static constexpr int NW = WGM * WGN;           // waves per workgroup
+    static constexpr int NW = WGM * WGN * WGK;     // waves per workgroup
     static constexpr int NT = NW * 64;             // threads per workgroup
     static constexpr int WTM = BM / WGM, WTN = BN / WGN;  // wave tile
     static constexpr int FM = WTM / 32, FN = WTN / 32;    // 32x32 MFMA blocks per wave
@@ -86,7 +89,7 @@ struct TileCfg {
     static constexpr int A_PW = A_BLKS / NW, B_PW = B_BLKS / NW;  // DMA blocks per wave
     static constexpr int LOADS = A_PW + B_PW;      // DMA instructions per wave per stage
     static constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
-    static constexpr int KSTEPS = BK / 16;         // MFMA k-steps per stage
+    static constexpr int KSTEPS = BK / 16 / WGK;   // MFMA k-steps per stage and wave
     // Output staging of the epilogue: from stage STAGES-1 (which the next unit's DMA prologue
     // leaves free) up to EPI_AVAIL bytes.  A workgroup whose stages take more than half of the
     // LDS runs alone on its CU, so it may use all 160 KiB; a smaller one keeps to one stage and
@@ -103,15 +106,19 @@ struct TileCfg {
     }
     static constexpr int ER = er_pick();
     static constexpr int LDS_ALLOC = (EPI_OFF + ER * OUT_ROWB > LDS_BYTES) ? EPI_OFF + ER * OUT_ROWB : LDS_BYTES;
+    // LDS a workgroup allocates at most (a K-sliced tile exchanges its partials through the
+    // whole staging area)
+    static constexpr int LDS_USE = WGK > 1 ? EPI_OFF + EPI_AVAIL : LDS_ALLOC;
     static_assert(ER > 0, "no output chunk of whole 32-row blocks fits the staging area");
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
     static_assert(ROWB % 16 == 0 && CH >= 2, "BK must be a multiple of 16");
+    static_assert(BK % (16 * WGK) == 0, "every wave takes whole k-steps of a stage");
     static_assert(A_BLKS % NW == 0 && B_BLKS % NW == 0, "DMA blocks must split evenly over waves");
     static_assert(32 % (CH * R256) == 0, "fragment rows start on a swizzle period");
     static_assert(SWZ_PERIOD <= 2, "at most two DMA offset sets");
     static_assert(SWZ_PERIOD == 1 || (A_PW % 2 == 0 && B_PW % 2 == 0),
                   "block parity of every DMA instruction must be known at compile time");
-    static_assert(LDS_ALLOC <= LDS_MAX, "gfx950 has 160 KiB of LDS per CU");
+    static_assert(LDS_ALLOC <= LDS_MAX && LDS_USE <= LDS_MAX, "gfx950 has 160 KiB of LDS per CU");
 };
 
 // ---------------------------------------------------------------------------
@@ -318,10 +325,10 @@ struct UnitWalker {
 template <int DT, class C>
 struct Engine {
     static constexpr int FM = C::FM, FN = C::FN, NT = C::NT, S = C::STAGES, KS = C::KSTEPS;
-    static_assert(KS % 2 == 0, "fragment double-buffer assumes an even number of k-steps");
+    static_assert(KS % 2 == 0, "fragment double-buffer assumes an even number of k-steps per wave");
 
     lds_char* smem;
-    int tid, lane, wave, wm, wn;
+    int tid, lane, wave, wm, wn, wk;
     int a_row_off, b_row_off;  // per-lane LDS byte offsets of the fragment rows
     int swz;                   // chunk XOR of this lane's fragment rows
     static __device__ __forceinline__ int swz_of(int row) { return (row / C::R256) % C::CH; }
@@ -331,11 +338,13 @@ struct Engine {
         lane = tid & 63;
         wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         wm = wave % C::WGM;
-        wn = wave / C::WGM;
+        wn = C::WGK == 1 ? wave / C::WGM : (wave / C::WGM) % C::WGN;
+        wk = C::WGK == 1 ? 0 : wave / (C::WGM * C::WGN);
         const int r = lane & 31;
         a_row_off = (wm * C::WTM + r) * C::ROWB;
         b_row_off = C::A_BYTES + (wn * C::WTN + r) * C::ROWB;
         swz = swz_of(r);
+        khalf = 2 * KS * wk + (lane >> 5);
     }
 
     __device__ __forceinline__ void rsrc(const GemmParams& p, const Unit& u,
@@ -453,23 +462,29 @@ struct Engine {
         }
     }
 
-    // The first min(S-1, n) K-iterations of a unit go to stages 0, 1, ...; iteration S-1+it is
-    // fetched during iteration it.
+    // K-iterations 0..S-2 of a unit go to stages 0..S-2; iteration S-1+it is fetched during
+    // iteration it.  A unit shorter than S-1 iterations still issues all S-1 stages (zeros past
+    // its end): the epilogue then knows that exactly the last LOADS*(S-1) loads of a wave
+    // belong to the next unit, and that every load before them -- the zero fills of the
+    // current unit's last iterations included -- has to land before the staging area is
+    // written.
     __device__ __forceinline__ void prologue(const GemmParams& p, const Unit& u) const {
         __amdgpu_buffer_rsrc_t ra, rb;
         rsrc(p, u, ra, rb);
         const DmaLane L = dma_lane(p);
 #pragma unroll
         for (int s = 0; s < S - 1; ++s)
-            if (u.kb + s < u.ke) issue_range<false, 0, C::LOADS>(p, ra, rb, s, L, dma_it(p, u.kb + s, true));
+            issue_range<false, 0, C::LOADS>(p, ra, rb, s, L, dma_it(p, u.kb + s, u.kb + s < u.ke));
     }
 
     // Fragment registers: A (activation rows) double-buffered across k-steps, B (weight rows)
     // reloaded in place right after its last use, which the j-major MFMA order makes early.
     u32x4 fa[2][FM], fb[FN];
 
+    // byte offset in its row of this lane's 16-byte K chunk for k-step ks of the wave's slice
+    int khalf;  // 2 * (first k-step of the wave's slice) + (lane >> 5)
     __device__ __forceinline__ int frag_chunk(int ks) const {
-        return ((2 * ks + (lane >> 5)) ^ swz) * 16;
+        return ((2 * ks + khalf) ^ swz) * 16;
     }
     template <int BUF, int I>
     __device__ __forceinline__ void read_a(int stage, int ks) {
@@ -521,7 +536,7 @@ struct Engine {
     static constexpr int DMA_SLOTS = (S == 2)  ? (C::DMAKS > 0 ? C::DMAKS : KS / 2) * NM
                                      : DMA_ALL ? KS * NM
                                                : (KS - 1) * NM + SYNC_Q;
-    static_assert(KS >= 2 && DMA_SLOTS >= 1, "at least two k-steps per stage");
+    static_assert(DMA_SLOTS >= 1, "at least one slot carries the refill");
     // loads of the current iteration's group issued before the stage wait (after the MFMA and
     // before the DMA of slot SYNC_Q of the last k-step)
     static constexpr int DMA_BEFORE_WAIT =
@@ -607,6 +622,19 @@ struct Engine {
         }
     }
 
+    // One iteration `it` of a unit that refills stage cur-1 with iteration it+S-1 (zeros past
+    // the unit), then advances cur.
+    template <bool FAST>
+    __device__ __forceinline__ void step(const GemmParams& p, const Unit& u, const Unit& nx,
+                                         const __amdgpu_buffer_rsrc_t& ra, const __amdgpu_buffer_rsrc_t& rb,
+                                         const DmaLane& L, f32x16 (&acc)[FN][FM], int& cur, int it, int n) {
+        const int dkit = it + S - 1;
+        const DmaIt o = dma_it(p, u.kb + dkit, FAST || dkit < n);
+        const int dstage = (cur == 0) ? S - 1 : cur - 1;
+        ksteps<FAST, false, 0>(p, nx, ra, rb, cur, dstage, L, o, acc);
+        cur = (cur + 1 == S) ? 0 : cur + 1;
+    }
+
     // acc = sum over K-iterations [u.kb, u.ke) of tile (u.tm, u.tn).  On entry the DMA prologue
     // of the unit is in flight, possibly behind the previous unit's stores, so the first wait
     // drains everything.  Iteration it fetches iteration it+S-1 into the stage freed at the end
@@ -636,20 +664,9 @@ struct Engine {
         if constexpr (FASTK) {
             const bool interior = (u.tm + 1) * C::BM <= p.m_valid && (u.tn + 1) * C::BN <= p.n_valid;
             const int fast_end = interior ? max(0, min(n, p.K / C::BK - u.kb) - (S - 1)) : 0;
-            for (; it < fast_end && it < n - 1; ++it) {
-                const DmaIt o = dma_it(p, u.kb + it + S - 1, true);
-                const int dstage = (cur == 0) ? S - 1 : cur - 1;
-                ksteps<true, false, 0>(p, nx, ra, rb, cur, dstage, L, o, acc);
-                cur = (cur + 1 == S) ? 0 : cur + 1;
-            }
+            for (; it < fast_end && it < n - 1; ++it) step<true>(p, u, nx, ra, rb, L, acc, cur, it, n);
         }
-        for (; it < n - 1; ++it) {
-            const int dkit = it + S - 1;
-            const DmaIt o = dma_it(p, u.kb + dkit, dkit < n);
-            const int dstage = (cur == 0) ? S - 1 : cur - 1;
-            ksteps<false, false, 0>(p, nx, ra, rb, cur, dstage, L, o, acc);
-            cur = (cur + 1 == S) ? 0 : cur + 1;
-        }
+        for (; it < n - 1; ++it) step<false>(p, u, nx, ra, rb, L, acc, cur, it, n);
         ksteps<false, true, 0>(p, nx, ra, rb, cur, 0, L, DmaIt{0u, 0}, acc);
     }
 
@@ -771,8 +788,9 @@ struct Engine {
     // words of group 2p+1, after which lane l < 32 holds columns 16p + 0..7 and lane l + 32
     // columns 16p + 8..15 of the same row: every 32x32 block leaves in two 16-byte stores per
     // lane (32 rows x 32 contiguous bytes per instruction), with no LDS round trip and no
-    // barrier, so the next unit's main loop starts as soon as the stores are issued.
-    template <int EPI>
+    // barrier, so the next unit's main loop starts as soon as the stores are issued.  Row
+    // blocks [I0, I1) of the wave tile are stored.
+    template <int EPI, int I0 = 0, int I1 = FM>
     __device__ __forceinline__ void store_tile_regs(const GemmParams& p, const Unit& u,
                                                     f32x16 (&acc)[FN][FM]) const {
         int ln = lane;
@@ -780,7 +798,7 @@ struct Engine {
         const int m0 = u.tm * C::BM + wm * C::WTM + (ln & 31);
         const int n0 = u.tn * C::BN + wn * C::WTN + 8 * (ln >> 5);
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
+        for (int i = I0; i < I1; ++i) {
             const int m = m0 + 32 * i;
             char* row = (char*)p.c + (size_t)m * (size_t)p.ldc * 2;
 #pragma unroll
@@ -801,6 +819,77 @@ struct Engine {
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
+    }
+
+    // ---- epilogue of a K-sliced tile (two waves along K) ------------------------------------
+    // The two slices of a wave tile hold FP32 partial sums over the two halves of every stage.
+    // Slice WK owns row blocks [WK*IH, (WK+1)*IH) (all j).  Each slice writes the blocks its
+    // partner owns into the free stage(s) in register order -- 16-byte group q of block b at
+    // ((b*4 + q)*64 + lane)*16 of the wave's area, so every ds_write_b128 / ds_read_b128 is one
+    // contiguous 1 KiB -- the partner adds them to its own, and each slice then activates,
+    // casts and stores its blocks from registers.  A sum of two FP32 terms does not depend on
+    // which slice adds, so the result is bit-reproducible.  The exchange goes in phases of XB
+    // blocks per wave when the area is smaller than the blocks to send.
+    static constexpr int IH = FM / 2;                     // row blocks owned by each slice
+    static constexpr int XBLK = FN * IH;                  // blocks a wave sends
+    static constexpr int XPW = C::EPI_AVAIL / C::NW;      // exchange bytes per wave
+    static constexpr int XB = XPW / 4096 < XBLK ? XPW / 4096 : XBLK;  // blocks per phase
+    static_assert(C::WGK == 1 || (C::WGK == 2 && FM % 2 == 0 && XB >= 1),
+                  "K slicing: two slices, an even number of row blocks, room for one block per wave");
+
+    template <int BASE, int B0, int B1>
+    __device__ __forceinline__ void xsend(lds_char* area, f32x16 (&acc)[FN][FM]) const {
+        if constexpr (B0 < B1) {
+            constexpr int j = B0 / IH, i = BASE + B0 % IH, sl = B0 % XB;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                *(__attribute__((address_space(3))) f32x4*)(area + ((sl * 4 + q) * 64 + lane) * 16) =
+                    f32x4{acc[j][i][4 * q], acc[j][i][4 * q + 1], acc[j][i][4 * q + 2], acc[j][i][4 * q + 3]};
+            xsend<BASE, B0 + 1, B1>(area, acc);
+        }
+    }
+    template <int BASE, int B0, int B1>
+    __device__ __forceinline__ void xrecv(const lds_char* area, f32x16 (&acc)[FN][FM]) const {
+        if constexpr (B0 < B1) {
+            constexpr int j = B0 / IH, i = BASE + B0 % IH, sl = B0 % XB;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const f32x4 v = *(const __attribute__((address_space(3))) f32x4*)(area + ((sl * 4 + q) * 64 + lane) * 16);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) acc[j][i][4 * q + c] += v[c];
+            }
+            xrecv<BASE, B0 + 1, B1>(area, acc);
+        }
+    }
+    template <int WK, int PH>
+    __device__ __forceinline__ void xphases(f32x16 (&acc)[FN][FM]) const {
+        if constexpr (PH * XB < XBLK) {
+            constexpr int b0 = PH * XB, b1 = (PH + 1) * XB < XBLK ? (PH + 1) * XB : XBLK;
+            const int partner = wave + (WK == 0 ? 1 : -1) * C::WGM * C::WGN;
+            if constexpr (PH > 0) barrier();  // the partner has read the previous phase
+            xsend<(1 - WK) * IH, b0, b1>(smem + C::EPI_OFF + wave * XPW, acc);
+            barrier();
+            xrecv<WK * IH, b0, b1>(smem + C::EPI_OFF + partner * XPW, acc);
+            xphases<WK, PH + 1>(acc);
+        }
+    }
+    template <int EPI, int WK>
+    __device__ __forceinline__ void store_sliced_as(const GemmParams& p, const Unit& u, bool next,
+                                                    f32x16 (&acc)[FN][FM]) {
+        // DMA still in flight may target any stage but the next unit's prologue (issued last):
+        // drain it; the barrier makes sure every wave has before the area is written
+        if (next) wait_vmcnt<C::LOADS * (S - 1)>();
+        else wait_vmcnt<0>();
+        barrier();
+        xphases<WK, 0>(acc);
+        store_tile_regs<EPI, WK * IH, (WK + 1) * IH>(p, u, acc);
+    }
+    template <int EPI>
+    __device__ __forceinline__ void store_sliced(const GemmParams& p, const Unit& u, bool next,
+                                                 f32x16 (&acc)[FN][FM]) {
+        // one static body per slice (acc is dead after either)
+        if (wk == 0) store_sliced_as<EPI, 0>(p, u, next, acc);
+        else store_sliced_as<EPI, 1>(p, u, next, acc);
     }
 
     // FP32 partial tile in the accumulator's own register order: group (j, i, q) of thread
@@ -831,8 +920,12 @@ __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
     // workgroup stores at once.  The Stream-K kernel, whose split pieces leave through
     // store_partial, stores its whole tiles from registers too: the staging registers would
     // push it past 256 VGPRs.
+    // A K-sliced tile exchanges its partial sums through the free stage(s) and stores from
+    // registers (it has no Stream-K form: its split pieces would need the exchange first).
+    static_assert(C::WGK == 1 || !SK, "no Stream-K form of a K-sliced tile");
     constexpr bool EPI_IN_REGS = EPI != EPI_STORE || SK;
-    __shared__ __attribute__((aligned(1024))) char smem_raw[EPI_IN_REGS ? C::LDS_BYTES : C::LDS_ALLOC];
+    constexpr int SMEM = C::WGK > 1 ? C::LDS_USE : EPI_IN_REGS ? C::LDS_BYTES : C::LDS_ALLOC;
+    __shared__ __attribute__((aligned(1024))) char smem_raw[SMEM];
     Engine<DT, C> eng((lds_char*)smem_raw, p);
     f32x16 acc[C::FN][C::FM];
 
@@ -851,6 +944,8 @@ __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
         eng.template mainloop<FASTK>(p, u, nx, acc);
         if (SK && u.split >= 0)
             eng.store_partial(sk_slot(p, v, u.local, C::BM * C::BN), acc);
+        else if constexpr (C::WGK > 1)
+            eng.template store_sliced<EPI>(p, u, nx.valid, acc);
         else if constexpr (EPI_IN_REGS)
             eng.template store_tile_regs<EPI>(p, u, acc);
         else

@@ -28,42 +28,50 @@ using Cfg = VariantCfg<FFN_VARIANT>::type;
 
 namespace {
 // one launch of ffn_gemm_kernel with the DMA addressing the plan chose
-template <int EPI, bool SK>
+template <class CFG, int EPI, bool SK>
 void launch_gemm(const ffn::GemmParams* p, dim3 g, dim3 b, hipStream_t stream) {
     if (p->fast_dma)
-        hipLaunchKernelGGL((ffn::ffn_gemm_kernel<FFN_DT, Cfg, EPI, SK, true>), g, b, 0, stream, *p);
+        hipLaunchKernelGGL((ffn::ffn_gemm_kernel<FFN_DT, CFG, EPI, SK, true>), g, b, 0, stream, *p);
     else
-        hipLaunchKernelGGL((ffn::ffn_gemm_kernel<FFN_DT, Cfg, EPI, SK, false>), g, b, 0, stream, *p);
+        hipLaunchKernelGGL((ffn::ffn_gemm_kernel<FFN_DT, CFG, EPI, SK, false>), g, b, 0, stream, *p);
 }
-}  // namespace
 
-extern "C" hipError_t FFN_LAUNCHER(int role, const ffn::GemmParams* p, int grid, hipStream_t stream) {
+template <class CFG>
+hipError_t launch_role(int role, const ffn::GemmParams* p, int grid, hipStream_t stream) {
     using namespace ffn;
-    const dim3 g(grid), b(Cfg::NT);
+    const dim3 g(grid), b(CFG::NT);
     switch (role) {
         case FFN_ROLE_UP_ERF:
-            launch_gemm<EPI_GELU_ERF, false>(p, g, b, stream);
+            launch_gemm<CFG, EPI_GELU_ERF, false>(p, g, b, stream);
             break;
         case FFN_ROLE_UP_RATIONAL:
-            launch_gemm<EPI_GELU_RATIONAL, false>(p, g, b, stream);
+            launch_gemm<CFG, EPI_GELU_RATIONAL, false>(p, g, b, stream);
             break;
         case FFN_ROLE_DOWN_BASIC:
-            launch_gemm<EPI_STORE, false>(p, g, b, stream);
+            launch_gemm<CFG, EPI_STORE, false>(p, g, b, stream);
             break;
-        case FFN_ROLE_DOWN_STREAMK: {
-            launch_gemm<EPI_STORE, true>(p, g, b, stream);
-            if (p->sk_tiles > 0) {
-                // one reduce workgroup per 32x32 accumulator block of each split tile: every
-                // partial load of the fixup is then in flight at once (a workgroup walking
-                // several blocks serialises their memory latencies)
-                constexpr int blocks = Cfg::FN * Cfg::FM;
-                hipLaunchKernelGGL((ffn_sk_reduce_kernel<FFN_DT, Cfg>), dim3(p->sk_tiles * blocks), b, 0,
-                                   stream, *p, blocks);
+        case FFN_ROLE_DOWN_STREAMK:
+            if constexpr (CFG::WGK > 1) {
+                return hipErrorInvalidValue;  // a K-sliced tile has no Stream-K form
+            } else {
+                launch_gemm<CFG, EPI_STORE, true>(p, g, b, stream);
+                if (p->sk_tiles > 0) {
+                    // one reduce workgroup per 32x32 accumulator block of each split tile:
+                    // every partial load of the fixup is then in flight at once (a workgroup
+                    // walking several blocks serialises their memory latencies)
+                    constexpr int blocks = CFG::FN * CFG::FM;
+                    hipLaunchKernelGGL((ffn_sk_reduce_kernel<FFN_DT, CFG>), dim3(p->sk_tiles * blocks), b,
+                                       0, stream, *p, blocks);
+                }
             }
             break;
-        }
         default:
             return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+}  // namespace
+
+extern "C" hipError_t FFN_LAUNCHER(int role, const ffn::GemmParams* p, int grid, hipStream_t stream) {
+    return launch_role<Cfg>(role, p, grid, stream);
 }

@@ -39,13 +39,17 @@ namespace {
 struct Variant {
     int bm, bn, bk, wgm, wgn, stages;
     int lds_bytes;            // LDS of one workgroup: the stages plus any epilogue staging beyond
+    int nw;                   // waves per workgroup
+    int wgk;                  // waves along K (K-sliced tile when > 1)
     ffn_launch_fn launch[2];  // [dtype]
-    int waves() const { return wgm * wgn; }
+    int waves() const { return nw; }
     int lds() const { return lds_bytes; }
 };
 
-#define FFN_VARIANT_ROW(id, bm, bn, bk, wgm, wgn, st, ...)                                       \
-    {bm, bn, bk, wgm, wgn, st, ffn::TileCfg<bm, bn, bk, wgm, wgn, st, ##__VA_ARGS__>::LDS_ALLOC, \
+#define FFN_VARIANT_ROW(id, bm, bn, bk, wgm, wgn, st, ...)                                     \
+    {bm, bn, bk, wgm, wgn, st, ffn::TileCfg<bm, bn, bk, wgm, wgn, st, ##__VA_ARGS__>::LDS_USE, \
+     ffn::TileCfg<bm, bn, bk, wgm, wgn, st, ##__VA_ARGS__>::NW,                                \
+     ffn::TileCfg<bm, bn, bk, wgm, wgn, st, ##__VA_ARGS__>::WGK,                               \
      {ffn_launch_d0_v##id, ffn_launch_d1_v##id}},
 const Variant kVariants[] = {FFN_VARIANTS(FFN_VARIANT_ROW)};
 #undef FFN_VARIANT_ROW
@@ -85,9 +89,11 @@ constexpr double kReduceRate = 3.0e12;     // B/s of the fixup kernel
 constexpr double kUnitOverhead = 2.5e-6;   // s per unit: DMA prologue latency + epilogue
 
 // Relative MFMA efficiency of each macro tile (measured on the FFN shapes, 256x256 = 1): the
-// fragment reads per MFMA grow as the wave tile shrinks.
+// fragment reads per MFMA grow as the wave tile shrinks.  A K-sliced 128x128 tile has 128x64
+// wave tiles (and pays an LDS exchange of half its partials per tile).
 double tile_eff(const Variant& v) {
     const int a = v.bm < v.bn ? v.bm : v.bn, b = v.bm < v.bn ? v.bn : v.bm;
+    if (v.wgk > 1) return 0.85;
     if (a >= 256) return 1.0;
     if (a == 128 && b == 256) return 0.95;
     if (a == 128) return 0.6;
@@ -168,7 +174,7 @@ int pick_streamk(long long M, long long m_valid, long long N, long long K, int G
     double best_cost = 1e300;
     for (int i = 0; i < kNumVariants; ++i) {
         SkShape s;
-        if (!sk_shape(kVariants[i], M, N, K, G, s)) continue;
+        if (kVariants[i].wgk > 1 || !sk_shape(kVariants[i], M, N, K, G, s)) continue;
         const double c = cost_streamk(kVariants[i], s, m_valid, N, K, G);
         if (c < best_cost * 0.999) best_cost = c, best = i;
     }
@@ -276,6 +282,10 @@ int ffn_mi355x_make_plan(int m, int mp, int kp, int hp, int np, int dtype, int d
     if (down_impl == FFN_MI355X_DOWN_STREAMK) {
         if (down_variant >= 0) {
             SkShape s;
+            if (kVariants[down_variant].wgk > 1)
+                return fail(FFN_MI355X_ENOT_APPLICABLE,
+                            "Stream-K candidate: tile variant %d is K-sliced and has no Stream-K form",
+                            down_variant);
             if (!sk_shape(kVariants[down_variant], mp, np, hp, G, s)) {
                 if (s.k_iters < 2)
                     return fail(FFN_MI355X_ENOT_APPLICABLE,

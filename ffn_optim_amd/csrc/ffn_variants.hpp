@@ -1,27 +1,32 @@
 // ffn_variants.hpp -- the macro-tile variants compiled into libffn_mi355x.so.
 //
-// X(id, BM, BN, BK, waves along M, waves along N, LDS stages[, sync slot, DMA k-steps])
+// X(id, BM, BN, BK, waves along M, waves along N, LDS stages[, sync slot, DMA k-steps,
+//   waves along K])
 // (DMA k-steps equal to the k-steps per stage spreads a deep pipeline's refill over the
-// whole iteration.)
+// whole iteration.)  The K-sliced 128x128 tiles (10, 11) give each wave a 128x64 wave tile
+// over half of every stage: a quarter fewer fragment reads per MFMA than 64x64 wave tiles,
+// for the down GEMMs whose output has about one 128x128 tile per CU.
 // The deep-pipeline 64-row tiles (8, 9) keep 56 KiB or more of weights in flight per CU for
 // the memory-bound small-M (decode) shapes.
 // Each variant is built for both storage types and four epilogues (GELU-erf,
 // GELU-rational, plain store, plain store + Stream-K split) in its own object.
 #pragma once
 
-#define FFN_VARIANTS(X)                 \
-    X(0, 256, 256, 64, 2, 2, 2, 9)      \
-    X(1, 256, 128, 64, 2, 2, 3)         \
-    X(2, 128, 256, 64, 2, 2, 3)         \
-    X(3, 128, 128, 64, 2, 2, 2)         \
-    X(4, 64, 64, 64, 2, 2, 2)           \
-    X(5, 64, 128, 64, 2, 2, 3)          \
-    X(6, 256, 256, 32, 2, 2, 4, -1, 2)  \
-    X(7, 256, 256, 32, 2, 2, 5, -1, 2)  \
-    X(8, 64, 64, 64, 2, 2, 8, -1, 4)    \
-    X(9, 64, 128, 64, 2, 2, 6)
+#define FFN_VARIANTS(X)                     \
+    X(0, 256, 256, 64, 2, 2, 2, 9)          \
+    X(1, 256, 128, 64, 2, 2, 3)             \
+    X(2, 128, 256, 64, 2, 2, 3)             \
+    X(3, 128, 128, 64, 2, 2, 2)             \
+    X(4, 64, 64, 64, 2, 2, 2)               \
+    X(5, 64, 128, 64, 2, 2, 3)              \
+    X(6, 256, 256, 32, 2, 2, 4, -1, 2)      \
+    X(7, 256, 256, 32, 2, 2, 5, -1, 2)      \
+    X(8, 64, 64, 64, 2, 2, 8, -1, 4)        \
+    X(9, 64, 128, 64, 2, 2, 6)              \
+    X(10, 128, 128, 64, 1, 2, 5, -1, 2, 2)  \
+    X(11, 128, 128, 64, 1, 2, 4, -1, 2, 2)
 
-#define FFN_NUM_VARIANTS 10
+#define FFN_NUM_VARIANTS 12
 
 
 // launch roles of one variant

@@ -259,3 +259,24 @@ def test_set_operands_validates_layout():
         with pytest.raises(ValueError):
             _lib.set_operands(plan, *bad)
         assert (plan.k, plan.h, plan.n) == (1000, 3001, 999)
+
+
+def test_k_sliced_variants_basic_only():
+    """The K-sliced 128x128 tiles (two waves along K) are planned for the Basic down and the up
+    GEMM, report four waves, and have no Stream-K form."""
+    from ffn_optim_amd import _lib
+    from ffn_optim_amd.host.dispatch import NotApplicable
+    sliced = [v for v in _lib.variants() if v["bm"] == 128 and v["bn"] == 128 and v["stages"] >= 4]
+    assert sliced, "no K-sliced variant compiled in"
+    for v in sliced:
+        assert v["waves"] == 4 and v["lds_bytes"] == 160 * 1024
+        plan = _lib.make_plan(4096, 1024, 4096, 1024, _lib.BF16, "basic", "erf", 256,
+                              v["variant"], v["variant"])
+        assert (plan.up_variant, plan.down_variant) == (v["variant"], v["variant"])
+        assert plan.workspace_bytes == 0
+        with pytest.raises(NotApplicable, match="K-sliced"):
+            _lib.make_plan(4096, 1024, 4096, 1024, _lib.BF16, "streamk", "erf", 256, 0, v["variant"])
+    # the planner's own Stream-K choice never lands on one
+    for mp, np_ in ((4096, 1024), (1024, 1024), (8192, 3072)):
+        plan = _lib.make_plan(mp, 1024, 4096, np_, _lib.BF16, "streamk", "erf", 256)
+        assert plan.down_variant not in {v["variant"] for v in sliced}
