@@ -63,12 +63,21 @@ def workload_numbers(case):
     }
 
 
+WARM_SECONDS = 0.2   # warmup floor: the GPU leaves its idle clocks within tens of milliseconds
+
+
 def time_events(fn, steps, warmup, stream=None, flush=None):
-    """Median and mean per-call device time (ms) with events on the current stream."""
+    """Median and mean per-call device time (ms) with events on the current stream, after
+    `warmup` untimed calls and at least WARM_SECONDS of untimed calls."""
     import torch
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    t_end = time.perf_counter() + WARM_SECONDS
+    while time.perf_counter() < t_end:
+        for _ in range(8):
+            fn()
+        torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     if flush is None:
         start.record()
@@ -287,6 +296,7 @@ def main(argv=None):
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_floor_s": WARM_SECONDS,
         "ms_per_step": best["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
