@@ -34,9 +34,9 @@ class PreparedFFN:
     """Prepared inputs, buffers and bound kernels; run() may be called repeatedly.
 
     storage is (X[mp,kp], W1[hp,kp], W2[np,hp], hidden[mp,hp], out[mp,np], ws) on
-    one device (for ffn(), operands read in place keep their own shapes); tensors holds their device addresses; provenance and preparation
-    record the library and the preparation timings; stream is the preparation
-    stream (ops/api.py:17-35).
+    one device (for ffn(), operands read in place keep their own shapes); tensors
+    holds their device addresses; provenance and preparation record the library and
+    the preparation timings; stream is the preparation stream (ops/api.py:17-35).
     """
 
     plan: object

@@ -202,11 +202,16 @@ bool layout_ok(const ffn_mi355x_plan* p) {
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
+bool plan_derivation_matches(const ffn_mi355x_plan* p);
+
+// A plan is used only as ffn_mi355x_make_plan (and ffn_mi355x_set_operands) left it: the grids,
+// tile counts, Stream-K split and workspace size it carries decide which memory the kernels
+// touch, so they are derived again from the plan's own inputs and must match.
 bool valid_plan(const ffn_mi355x_plan* p) {
     return p && p->m >= 1 && p->m <= p->mp && layout_ok(p) && p->up_variant >= 0 && p->up_variant < kNumVariants && p->down_variant >= 0 &&
            p->down_variant < kNumVariants && (p->dtype == 0 || p->dtype == 1) &&
            (p->down_impl == FFN_MI355X_DOWN_BASIC || p->down_impl == FFN_MI355X_DOWN_STREAMK) &&
-           (p->gelu == 0 || p->gelu == 1) && p->block_num >= 1;
+           (p->gelu == 0 || p->gelu == 1) && p->block_num >= 1 && plan_derivation_matches(p);
 }
 
 int launch(const Variant& v, int dtype, int role, const ffn::GemmParams& gp, int grid,
@@ -346,6 +351,27 @@ int ffn_mi355x_set_operands(ffn_mi355x_plan* plan, int k, int h, int n, int ldx,
     return ok();
 }
 
+
+}  // extern "C"
+
+namespace {
+bool plan_derivation_matches(const ffn_mi355x_plan* p) {
+    ffn_mi355x_plan q;
+    const std::string saved = g_error;
+    const int rc = ffn_mi355x_make_plan(p->m, p->mp, p->kp, p->hp, p->np, p->dtype, p->down_impl, p->gelu,
+                                        p->block_num, p->up_variant, p->down_variant, &q);
+    g_error = saved;
+    return rc == FFN_MI355X_OK && q.up_variant == p->up_variant && q.down_variant == p->down_variant &&
+           q.up_bm == p->up_bm && q.up_bn == p->up_bn && q.up_bk == p->up_bk && q.down_bm == p->down_bm &&
+           q.down_bn == p->down_bn && q.down_bk == p->down_bk && q.up_tiles == p->up_tiles &&
+           q.up_grid == p->up_grid && q.down_tiles == p->down_tiles && q.down_grid == p->down_grid &&
+           q.down_k_iters == p->down_k_iters && q.down_dp_tiles == p->down_dp_tiles &&
+           q.down_sk_tiles == p->down_sk_tiles && q.down_slots_per_wg == p->down_slots_per_wg &&
+           q.workspace_bytes == p->workspace_bytes;
+}
+}  // namespace
+
+extern "C" {
 
 int ffn_mi355x_workspace_bytes(const ffn_mi355x_plan* plan, size_t* bytes) {
     if (!plan || !bytes) return fail(FFN_MI355X_EINVAL, "NULL argument");

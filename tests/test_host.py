@@ -280,3 +280,22 @@ def test_k_sliced_variants_basic_only():
     for mp, np_ in ((4096, 1024), (1024, 1024), (8192, 3072)):
         plan = _lib.make_plan(mp, 1024, 4096, np_, _lib.BF16, "streamk", "erf", 256)
         assert plan.down_variant not in {v["variant"] for v in sliced}
+
+
+def test_run_rejects_a_plan_whose_launch_fields_were_changed():
+    """ffn_mi355x_run / _up / _down re-derive a plan's grids, tile counts, Stream-K split and
+    workspace size from its inputs and refuse a plan that does not match (no launch is made,
+    so this runs without a GPU)."""
+    import ctypes
+    from ffn_optim_amd import _lib
+    lib = _lib.load()
+    fake = [ctypes.c_void_p(4096 * (i + 1)) for i in range(6)]  # aligned, never dereferenced
+    for down in ("basic", "streamk"):
+        for field, delta in (("up_grid", 1), ("down_grid", -1), ("down_slots_per_wg", -1),
+                             ("workspace_bytes", -256), ("down_sk_tiles", 1), ("up_bm", 64)):
+            plan = _lib.make_plan(1024, 1008, 3008, 1024, _lib.FP16, down, "erf", 256)
+            if down == "basic" and field in ("down_slots_per_wg", "workspace_bytes", "down_sk_tiles"):
+                continue
+            setattr(plan, field, getattr(plan, field) + delta)
+            rc = lib.ffn_mi355x_run(ctypes.byref(plan), *fake, None)
+            assert rc == -1 and "invalid plan" in lib.ffn_mi355x_last_error().decode(), (down, field)
