@@ -189,23 +189,22 @@ __device__ __forceinline__ u32x2 pack4(float a, float b, float c, float d) {
 // erfc uses the form of the Chebyshev fit of Press, Teukolsky, Vetterling & Flannery,
 // "Numerical Recipes in C" (2nd ed., sec. 6.2, erfcc):
 //     erfc(x) = t*exp(-x*x + P(t)),  t = 1/(1 + x/2),
-// with P of degree 7 fitted here (Lawson-reweighted least squares of log(erfc(x)/t) + x^2 in t
-// over x in [0, 10.5]; past that erfc is below the FP32 subnormals): relative error 6.5e-7 in
-// float64 and ~5e-6 in FP32 evaluation, where the rounding of x*x dominates (the degree-9 fit
-// does no better in FP32).  1/sqrt2, the factor 1/2 of h and the change to base 2 are folded
-// into the constants: one v_rcp_f32, one v_exp_f32 and about 12 full-rate VALU ops.  Like the
-// torch golden it returns NaN for z = +-inf and NaN.
+// with P of degree 5 fitted here (Lawson-reweighted least squares of log(erfc(x)/t) + x^2 in t
+// over x in [0, 10.5]; past that erfc is below the FP32 subnormals): relative error 7.6e-6 in
+// float64 and 1.1e-5 in FP32 evaluation, forty times below half an fp16 ulp.  (Degree 7 reaches
+// 4.6e-6 in FP32, where the rounding of x*x dominates, for two more FMAs per element: 1-3%
+// of an up GEMM.)  1/sqrt2, the factor 1/2 of h and the change to base 2 are folded into the
+// constants: one v_rcp_f32, one v_exp_f32 and about 10 full-rate VALU ops.  Like the torch
+// golden it returns NaN for z = +-inf and NaN.
 __device__ __forceinline__ float gelu_erf(float z) {
     constexpr float L2E = 1.4426950408889634f;                  // log2(e)
     const float a = __builtin_fabsf(z);
     const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(a, 0.35355339059327376f, 1.0f));  // 1/(1+|z|/(2 sqrt2))
-    float p = __builtin_fmaf(t, -0.1845742772f * L2E, 0.7379936207f * L2E);
-    p = __builtin_fmaf(t, p, -0.9773950853f * L2E);
-    p = __builtin_fmaf(t, p, 0.3279841365f * L2E);
-    p = __builtin_fmaf(t, p, -0.0281352906f * L2E);
-    p = __builtin_fmaf(t, p, 0.3905195168f * L2E);
-    p = __builtin_fmaf(t, p, 0.9991159075f * L2E);
-    p = __builtin_fmaf(t, p, -1.2655091784f * L2E - 1.0f);     // -1: the factor 1/2 of h
+    float p = __builtin_fmaf(t, 0.2287914322f * L2E, -0.7091943583f * L2E);
+    p = __builtin_fmaf(t, p, 0.4744972994f * L2E);
+    p = __builtin_fmaf(t, p, 0.2544409355f * L2E);
+    p = __builtin_fmaf(t, p, 1.0180141158f * L2E);
+    p = __builtin_fmaf(t, p, -1.2665418100f * L2E - 1.0f);     // -1: the factor 1/2 of h
     const float h = t * __builtin_amdgcn_exp2f(__builtin_fmaf(-a, a * (0.5f * L2E), p));  // -x^2 = -z^2/2
     // max(z, 0) as med3(z, 0, FLT_MAX): no NaN canonicalisation is needed, a NaN z already
     // makes |z| and the result NaN
