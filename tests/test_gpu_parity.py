@@ -283,3 +283,26 @@ def test_one_shot_ffn_in_place_matches_prepared(shape):
         torch.cuda.synchronize()
         assert torch.equal(again.view(torch.int16), ref.view(torch.int16))
         x.sub_(1.0)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_every_variant_at_logical_widths(dtype):
+    """Every compiled tile, forced for both GEMMs, on operands read in place at widths that
+    are not multiples of any tile (M=200 of 256, K=328, H=392, N=264): the reference
+    criterion against the golden, and bit-identical to the same tiles on padded copies."""
+    from ffn_optim_amd import ffn
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(33)
+    m, k, h, n = 200, 328, 392, 264
+    x = torch.randn(m, k, generator=g).to(dtype).cuda()
+    w1 = (torch.randn(h, k, generator=g) * k ** -0.5).to(dtype).cuda()
+    w2 = (torch.randn(n, h, generator=g) * h ** -0.5).to(dtype).cuda()
+    golden = ffn_torch(x.cpu(), w1.cpu(), w2.cpu())
+    for v in range(lib.ffn_mi355x_num_variants()):
+        say("variant at logical widths", dtype, v)
+        y = ffn(x, w1, w2, up_variant=v, down_variant=v)
+        ref = prepare_ffn(x, w1, w2, up_variant=v, down_variant=v).run()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), v
+        res = compare(y.cpu(), golden)
+        assert res["passed"], (v, res)
