@@ -127,18 +127,21 @@ def test_streamk_schedule_exact_once_and_slots(G):
             except ValueError:
                 continue
             kI, dp, sk = n.down_k_iters, n.down_dp_tiles, n.down_sk_tiles
-            assert dp + sk == n.down_tiles and sk == n.down_tiles % G and sk > 0
+            Gs = n.down_grid      # block_num, or fewer workgroups that cut every tile evenly
+            assert Gs <= G and (Gs == G or (n.down_tiles < G and Gs % n.down_tiles == 0
+                                            and kI % (Gs // n.down_tiles) == 0))
+            assert dp + sk == n.down_tiles and sk == n.down_tiles % Gs and sk > 0
             total = sk * kI
-            q, r = total // G, total % G
+            q, r = total // Gs, total % Gs
             seen = [[0] * kI for _ in range(sk)]
-            for v in range(G):
+            for v in range(Gs):
                 a, b = _sk_start(v, q, r), _sk_start(v + 1, q, r)
                 tiles = {it // kI for it in range(a, b)}
                 assert len(tiles) <= n.down_slots_per_wg
                 for it in range(a, b):
                     seen[it // kI][it % kI] += 1
             assert all(c == 1 for row in seen for c in row)
-            assert n.workspace_bytes == G * n.down_slots_per_wg * n.down_bm * n.down_bn * 4
+            assert n.workspace_bytes == Gs * n.down_slots_per_wg * n.down_bm * n.down_bn * 4
 
 
 def test_c_abi_exports_every_declared_symbol():
@@ -299,3 +302,12 @@ def test_run_rejects_a_plan_whose_launch_fields_were_changed():
             setattr(plan, field, getattr(plan, field) + delta)
             rc = lib.ffn_mi355x_run(ctypes.byref(plan), *fake, None)
             assert rc == -1 and "invalid plan" in lib.ffn_mi355x_last_error().decode(), (down, field)
+
+
+def test_streamk_grid_cuts_tiles_evenly_when_it_keeps_most_workgroups():
+    """Decode down (80 tiles of 64x64, 216 iterations each) at 256 workgroups: 240 workgroups
+    take one third of a tile each; C2's down (128 tiles, 64 iterations) keeps all 256."""
+    plan = _lib.make_plan(64, 5120, 13824, 5120, _lib.BF16, "streamk", "erf", 256, -1, 8, m=16)
+    assert (plan.down_tiles, plan.down_k_iters, plan.down_grid) == (80, 216, 240)
+    plan = _lib.make_plan(4096, 1024, 4096, 1024, _lib.BF16, "streamk", "erf", 256, -1, 2)
+    assert (plan.down_tiles, plan.down_k_iters, plan.down_grid) == (128, 64, 256)
