@@ -57,7 +57,9 @@ typedef struct ffn_mi355x_plan {
     int up_bm, up_bn, up_bk;     /* up-projection macro tile (M x H x K) */
     int down_bm, down_bn, down_bk; /* down-projection macro tile (M x N x H) */
     int up_tiles, up_grid;
-    int down_tiles, down_grid;
+    int down_tiles, down_grid;   /* down_grid <= block_num: fewer for Basic when there are fewer
+                                    tiles, and for Stream-K when that cuts every split tile into
+                                    equal pieces */
     int down_k_iters;            /* BK-deep iterations along H per down tile */
     int down_dp_tiles;           /* tiles reduced whole by one workgroup */
     int down_sk_tiles;           /* tiles whose H-range is split over workgroups */
