@@ -59,6 +59,7 @@ struct GemmParams {
     int slots_per_wg;     // partial-tile slots owned by each workgroup
     int group_m;          // tile-order swizzle: tiles walk group_m tile-rows column by column
     int fast_dma;         // 1: launch the kernel whose interior tiles refill through the SALU-addressed DMA path
+    int rev_m;            // 1: tile rows are walked last-first
 };
 
 // SYNCQ_: MFMA slot of a stage's last k-step after which the stage wait + barrier is placed
@@ -240,7 +241,9 @@ __device__ __forceinline__ float activate(float z) {
 }
 
 // tile index -> (tile row, tile column); tiles walk `group_m` tile-rows column by column so
-// that consecutive tiles share weight panels (columns) and activation panels (rows).
+// that consecutive tiles share weight panels (columns) and activation panels (rows).  With
+// rev_m the tile rows go last-first: the down GEMM then starts on the hidden rows the up GEMM
+// wrote last, the ones most likely still held by the 256 MiB last-level cache.
 __device__ __forceinline__ void tile_coords(const GemmParams& p, int t, int& tm, int& tn) {
     const int per_group = p.group_m * p.tiles_n;
     const int gidx = t / per_group;
@@ -249,6 +252,7 @@ __device__ __forceinline__ void tile_coords(const GemmParams& p, int t, int& tm,
     const int r = t - gidx * per_group;
     tm = first_m + r % rows;
     tn = r / rows;
+    if (p.rev_m) tm = p.tiles_m - 1 - tm;
 }
 
 // Split-region bookkeeping: split iteration x (0-based inside the split region) belongs to
