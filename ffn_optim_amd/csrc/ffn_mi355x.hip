@@ -219,6 +219,44 @@ bool layout_ok(const ffn_mi355x_plan* p) {
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
+// Bytes of a row-major buffer the kernels touch: `rows` rows at `pitch` elements, of which the
+// last is read or written only to `width` elements.
+size_t span_bytes(long long rows, long long pitch, long long width) {
+    return rows <= 0 ? 0 : (size_t)((rows - 1) * pitch + width) * 2u;
+}
+
+// [ptr, ptr + bytes) must lie inside one HIP allocation: a host pointer or a buffer too short
+// for the plan is refused before any launch instead of faulting the GPU.  Spans already checked
+// are remembered per thread, so repeated runs on the same buffers skip the lookup (a buffer
+// freed and reallocated smaller at the same address in between is not noticed).
+bool in_allocation(const void* ptr, size_t bytes) {
+    struct Seen {
+        const void* p;
+        size_t n;
+    };
+    thread_local Seen seen[16] = {};
+    thread_local int next = 0;
+    for (const Seen& e : seen)
+        if (e.p == ptr && e.n >= bytes) return true;
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    if (hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)ptr) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    const uintptr_t b = (uintptr_t)base, q = (uintptr_t)ptr;
+    if (q < b || bytes > size || q - b > size - bytes) return false;
+    seen[next] = Seen{ptr, bytes};
+    next = (next + 1) % 16;
+    return true;
+}
+
+int check_span(const char* name, const void* ptr, size_t bytes) {
+    if (in_allocation(ptr, bytes)) return FFN_MI355X_OK;
+    return fail(FFN_MI355X_EINVAL, "buffer %s at %p: %zu bytes needed are not inside one device allocation",
+                name, ptr, bytes);
+}
+
 bool plan_derivation_matches(const ffn_mi355x_plan* p);
 
 // A plan is used only as ffn_mi355x_make_plan (and ffn_mi355x_set_operands) left it: the grids,
@@ -402,6 +440,11 @@ int ffn_mi355x_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, vo
     if (!x || !w1 || !hidden) return fail(FFN_MI355X_EINVAL, "NULL device buffer");
     if (!aligned16(x) || !aligned16(w1) || !aligned16(hidden))
         return fail(FFN_MI355X_EINVAL, "device buffers must be 16-byte aligned");
+    int rc;
+    if ((rc = check_span("x", x, span_bytes(plan->m, plan->ldx, plan->k))) != FFN_MI355X_OK ||
+        (rc = check_span("w1", w1, span_bytes(plan->h, plan->ldw1, plan->k))) != FFN_MI355X_OK ||
+        (rc = check_span("hidden", hidden, span_bytes(plan->mp, plan->hp, plan->hp))) != FFN_MI355X_OK)
+        return rc;
     const Variant& U = kVariants[plan->up_variant];
     ffn::GemmParams gp;
     memset(&gp, 0, sizeof gp);
@@ -425,6 +468,13 @@ int ffn_mi355x_down(const ffn_mi355x_plan* plan, const void* hidden, const void*
     if (!hidden || !w2 || !out) return fail(FFN_MI355X_EINVAL, "NULL device buffer");
     if (!aligned16(hidden) || !aligned16(w2) || !aligned16(out) || (ws && !aligned16(ws)))
         return fail(FFN_MI355X_EINVAL, "device buffers must be 16-byte aligned");
+    int rc;
+    if ((rc = check_span("hidden", hidden, span_bytes(plan->m, plan->hp, down_depth(plan)))) != FFN_MI355X_OK ||
+        (rc = check_span("w2", w2, span_bytes(plan->n, plan->ldw2, down_depth(plan)))) != FFN_MI355X_OK ||
+        (rc = check_span("out", out, span_bytes(plan->mp, plan->np, plan->np))) != FFN_MI355X_OK ||
+        (plan->down_impl == FFN_MI355X_DOWN_STREAMK && ws &&
+         (rc = check_span("ws", ws, plan->workspace_bytes)) != FFN_MI355X_OK))
+        return rc;
     const Variant& D = kVariants[plan->down_variant];
     ffn::GemmParams gp;
     memset(&gp, 0, sizeof gp);

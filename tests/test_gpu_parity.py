@@ -306,3 +306,42 @@ def test_every_variant_at_logical_widths(dtype):
         assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), v
         res = compare(y.cpu(), golden)
         assert res["passed"], (v, res)
+
+
+def test_buffers_outside_their_allocation_are_refused():
+    """The C ABI checks every buffer's span against its device allocation before launching:
+    a host pointer or a buffer shorter than the plan needs returns an error, nothing runs."""
+    lib = _lib.load()
+    hip = ctypes.CDLL("libamdhip64.so.7")          # the runtime torch has already loaded
+    hip.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+    hip.hipMalloc.restype = ctypes.c_int
+    hip.hipFree.argtypes = [ctypes.c_void_p]
+    hip.hipFree.restype = ctypes.c_int
+    stream = torch.cuda.current_stream().cuda_stream
+    m, k, h, n = 4096, 64, 64, 4096                 # out is 32 MiB
+    plan = _lib.make_plan(m, k, h, n, _lib.BF16, "basic", "erf", 256)
+    x = torch.zeros(m, k, dtype=torch.bfloat16, device="cuda")
+    w1 = torch.zeros(h, k, dtype=torch.bfloat16, device="cuda")
+    w2 = torch.zeros(n, h, dtype=torch.bfloat16, device="cuda")
+    hidden = torch.zeros(m, h, dtype=torch.bfloat16, device="cuda")
+    out = torch.zeros(m, n, dtype=torch.bfloat16, device="cuda")
+    ptrs = [t.data_ptr() for t in (x, w1, w2, hidden, out)]
+    rc = lib.ffn_mi355x_run(ctypes.byref(plan), *ptrs, None, stream)
+    assert rc == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    # out in an allocation of its own holding half of what the plan writes
+    short = ctypes.c_void_p()
+    assert hip.hipMalloc(ctypes.byref(short), m * n) == 0
+    try:
+        rc = lib.ffn_mi355x_run(ctypes.byref(plan), *ptrs[:4], short.value, None, stream)
+        say("short out:", rc, _lib.last_error())
+        assert rc == -1 and "buffer out" in _lib.last_error()
+    finally:
+        torch.cuda.synchronize()
+        assert hip.hipFree(short) == 0
+    # X in host memory
+    host_x = torch.zeros(m, k, dtype=torch.bfloat16)
+    rc = lib.ffn_mi355x_run(ctypes.byref(plan), host_x.data_ptr(), *ptrs[1:], None, stream)
+    say("host x:", rc, _lib.last_error())
+    assert rc == -1 and "buffer x" in _lib.last_error()
+    torch.cuda.synchronize()
