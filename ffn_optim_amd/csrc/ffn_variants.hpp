@@ -16,7 +16,7 @@
 
 #define FFN_VARIANTS(X)                     \
     X(0, 256, 256, 64, 2, 2, 2, 9)          \
-    X(1, 256, 128, 64, 2, 2, 3)             \
+    X(1, 256, 128, 64, 2, 2, 3, -1, 4)      \
     X(2, 128, 256, 64, 2, 2, 3)             \
     X(3, 128, 128, 64, 2, 2, 2)             \
     X(4, 64, 64, 64, 2, 2, 2)               \
