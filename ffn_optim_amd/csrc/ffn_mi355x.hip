@@ -90,10 +90,11 @@ constexpr double kUnitOverhead = 2.5e-6;   // s per unit: DMA prologue latency +
 
 // Relative MFMA efficiency of each macro tile (measured on the FFN shapes, 256x256 = 1): the
 // fragment reads per MFMA grow as the wave tile shrinks.  A K-sliced 128x128 tile has 128x64
-// wave tiles (and pays an LDS exchange of half its partials per tile).
+// wave tiles (and pays an LDS exchange of half its partials per tile); with eight waves, two
+// per SIMD, one wave's MFMAs cover the other's waits.
 double tile_eff(const Variant& v) {
     const int a = v.bm < v.bn ? v.bm : v.bn, b = v.bm < v.bn ? v.bn : v.bm;
-    if (v.wgk > 1) return 0.85;
+    if (v.wgk > 1) return v.nw >= 8 ? 0.9 : 0.85;
     if (a >= 256) return 1.0;
     if (a == 128 && b == 256) return 0.95;
     if (a == 128) return 0.6;

@@ -5,7 +5,9 @@
 // (DMA k-steps equal to the k-steps per stage spreads a deep pipeline's refill over the
 // whole iteration.)  The K-sliced 128x128 tiles (10, 11) give each wave a 128x64 wave tile
 // over half of every stage: a quarter fewer fragment reads per MFMA than 64x64 wave tiles,
-// for the down GEMMs whose output has about one 128x128 tile per CU.  Variant 12 runs the
+// for the down GEMMs whose output has about one 128x128 tile per CU.  Variant 13 runs it with
+// eight waves (2x2 along M and N, 64x64 wave tiles), two per SIMD, so one wave's MFMAs cover
+// the other's LDS and barrier waits.  Variant 12 runs the
 // 256x256 tile with eight waves (two per SIMD, 128x64 wave tiles): when every CU holds a
 // single tile, the second wave of a SIMD issues MFMAs while the first waits on LDS or DMA.
 // The deep-pipeline 64-row tiles (8, 9) keep 56 KiB or more of weights in flight per CU for
@@ -27,9 +29,10 @@
     X(9, 64, 128, 64, 2, 2, 6)              \
     X(10, 128, 128, 64, 1, 2, 5, -1, 2, 2)  \
     X(11, 128, 128, 64, 1, 2, 4, -1, 2, 2)  \
-    X(12, 256, 256, 64, 2, 4, 2)
+    X(12, 256, 256, 64, 2, 4, 2)            \
+    X(13, 128, 128, 64, 2, 2, 4, -1, 2, 2)
 
-#define FFN_NUM_VARIANTS 13
+#define FFN_NUM_VARIANTS 14
 
 
 // launch roles of one variant

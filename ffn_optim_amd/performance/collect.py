@@ -49,6 +49,37 @@ def time_prepared(prepared, warmup=5, repeats=20, *, progress=None):
             "profiler_note": "Unavailable until a profiler trace is captured and inspected"}
 
 
+def time_interleaved(prepareds, rounds=9, batch=20, warmup=3):
+    """Round-robin timing of several prepared FFNs on their common preparation stream.
+
+    Each round times `batch` back-to-back run() calls of every candidate in turn with one
+    event pair, so the clock drift of a long search and the host's per-call launch gap
+    (which time_prepared's one-run event pairs include) do not decide between near-equal
+    candidates.  Returns each candidate's median over the rounds of the per-run mean, in us."""
+    if not prepareds or rounds < 1 or batch < 1 or warmup < 0:
+        raise ValueError("candidates, rounds >= 1, batch >= 1 and warmup >= 0 required")
+    import torch
+    device = prepareds[0].storage[0].device
+    means = [[] for _ in prepareds]
+    with torch.cuda.device(device):
+        for prepared in prepareds:
+            for _ in range(warmup):
+                prepared.run()
+        torch.cuda.synchronize(device)
+        for _ in range(rounds):
+            for slot, prepared in enumerate(prepareds):
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record()
+                for _ in range(batch):
+                    prepared.run()
+                end.record()
+                end.synchronize()
+                means[slot].append(start.elapsed_time(end) * 1000 / batch)
+    if any(not math.isfinite(v) or v <= 0 for row in means for v in row):
+        raise RuntimeError("Invalid device timing; refusing to rank these candidates")
+    return [statistics.median(row) for row in means]
+
+
 def capture_profile(prepared, directory):
     """Separate pass: record one FFN run with torch.profiler and export a Chrome trace to
     directory/trace.json (performance/collect.py:38-74).  Hardware counters need a

@@ -32,7 +32,8 @@ from ..cases import V1_CASES, case_problem, load_cases, make_inputs
 from ..host.dispatch import DependencyUnavailable, NotApplicable, Selection
 from ..host.tiling import DEFAULT_BLOCK_NUM, make_plan
 from .analyze import report
-from .tune import combinations, search, tile_space_down, tile_space_up
+from .tune import (combinations, pick_fastest, refine_candidates, search, tile_space_down,
+                   tile_space_up)
 
 REPO_ROOT = Path(__file__).resolve().parents[2]
 
@@ -177,7 +178,8 @@ class PerformanceRunner:
         _json(self.root / "accuracy.json", self.records)
         _json(self.root / "best_configs.json", self.bests)
         fields = ["case_id", "up_impl", "down_impl", "up_variant", "down_variant", "status",
-                  "device_median_us", "task_duration_us", "pipeline_utilization", "reason"]
+                  "device_median_us", "refined_median_us", "task_duration_us",
+                  "pipeline_utilization", "reason"]
         with (self.root / "performance.csv").open("w", newline="") as stream:
             writer = csv.DictWriter(stream, fieldnames=fields, extrasaction="ignore")
             writer.writeheader()
@@ -316,8 +318,7 @@ class PerformanceRunner:
         problem = case_problem(self.case)
         rows = [r for r in self.records[self.start_index:] if r["status"] == "passed"]
         for down in dict.fromkeys(r["configuration"]["down_impl"] for r in rows):
-            cands = [r for r in rows if r["configuration"]["down_impl"] == down]
-            fastest = min(cands, key=lambda r: r["device_median_us"])
+            fastest = pick_fastest([r for r in rows if r["configuration"]["down_impl"] == down])
             p = fastest["plan"]
             key = tuning.make_key(problem.m, p["mp"], p["kp"], p["hp"], p["np"], problem.dtype, down,
                                   self.args.gelu, self.block_num())
@@ -362,13 +363,42 @@ class PerformanceRunner:
         self.log(f"tune phase 2: {len(self.case_configs)} down variants with up v{up}")
         search(self.case_configs, self.evaluate, self.checkpoint)
         self.start_index = case_start
+        if self.args.execute_gpu and not self.args.validate_only:
+            self.refine(case_start)
         passed = [r for r in self.records[case_start:] if r["status"] == "passed"]
-        fastest = min(passed, key=lambda r: r["device_median_us"]) if passed else None
+        fastest = pick_fastest(passed)
         self.bests[case["case_id"]] = {
             "configuration": fastest["configuration"] if fastest else None,
             "device_median_us": fastest["device_median_us"] if fastest else None,
+            "refined_median_us": fastest.get("refined_median_us") if fastest else None,
             "complete": True, "ranking_metric": "unprofiled_device_event_median_us",
             "measured": bool(self.args.execute_gpu and not self.args.validate_only)}
+        self.persist()
+
+    def refine(self, case_start):
+        """Tune mode: re-time each down implementation's near-equal finalists side by side
+        (collect.time_interleaved) and store the result in their records as refined_median_us."""
+        import torch
+        from ..api import prepare_ffn
+        from .collect import time_interleaved
+        rows = [r for r in self.records[case_start:] if r["status"] == "passed"]
+        for down in dict.fromkeys(r["configuration"]["down_impl"] for r in rows):
+            finalists = refine_candidates([r for r in rows if r["configuration"]["down_impl"] == down])
+            if len(finalists) < 2:
+                continue
+            self.log(f"refining {down}: " + ", ".join(
+                f"up v{r['configuration']['up_variant']} down v{r['configuration']['down_variant']}"
+                for r in finalists) + " interleaved")
+            prepared = [prepare_ffn(*self.inputs, up_impl="basic", down_impl=down,
+                                    block_num=self.block_num(), layout=self.case.get("layout", "linear"),
+                                    gelu=self.args.gelu, up_variant=r["configuration"]["up_variant"],
+                                    down_variant=r["configuration"]["down_variant"]) for r in finalists]
+            for r, value in zip(finalists, time_interleaved(prepared)):
+                r["refined_median_us"] = value
+                self.log(f"  up v{r['configuration']['up_variant']} down v{r['configuration']['down_variant']}: "
+                         f"{value:.2f} us per run (back-to-back)")
+            del prepared
+            torch.cuda.synchronize(self.args.device)
         self.persist()
 
     def save_failure(self, exc):

@@ -4,7 +4,8 @@ combinations() builds the reference's implementation Cartesian product;
 tile_space_up()/tile_space_down() add the MI355X-specific dimension, the tile variants
 the library accepts for a problem, searched one GEMM at a time.  search() evaluates candidates in order, checkpoints after each
 one and ranks only candidates whose status is 'passed' with a finite positive
-unprofiled device-event median.
+unprofiled device-event median.  refine_candidates() picks the near-equal finalists that tune
+mode re-times side by side, and pick_fastest() ranks by that re-timing where it exists.
 """
 from __future__ import annotations
 
@@ -58,6 +59,33 @@ def tile_space_down(problem, downs, up_variant, block_num, gelu="erf"):
     return [{"up_impl": "basic", "down_impl": d, "up_variant": up_variant, "down_variant": dv}
             for d in dict.fromkeys(downs) for dv in range(nvar)
             if _applicable(problem, d, block_num, gelu, up_variant, dv) is not None]
+
+
+def refine_candidates(rows, within=0.05, limit=4):
+    """The passed records of one down implementation worth re-timing side by side: distinct
+    (up, down) variant pairs whose one-run median is within `within` of the fastest, at most
+    `limit`, fastest first."""
+    seen, out = set(), []
+    passed = sorted((r for r in rows if r.get("status") == "passed"), key=lambda r: r["device_median_us"])
+    for r in passed:
+        pair = (r["configuration"].get("up_variant"), r["configuration"].get("down_variant"))
+        if pair in seen or r["device_median_us"] > passed[0]["device_median_us"] * (1 + within):
+            continue
+        seen.add(pair)
+        out.append(r)
+    return out[:limit]
+
+
+def pick_fastest(rows):
+    """The record to keep among one down implementation's passed records: by the interleaved
+    re-timing (refined_median_us) where any record has one, else by the one-run median."""
+    passed = [r for r in rows if r.get("status") == "passed"]
+    if not passed:
+        return None
+    refined = [r for r in passed if isinstance(r.get("refined_median_us"), (int, float))]
+    if refined:
+        return min(refined, key=lambda r: r["refined_median_us"])
+    return min(passed, key=lambda r: r["device_median_us"])
 
 
 def search(configurations, evaluate, checkpoint=None):

@@ -266,13 +266,13 @@ def test_set_operands_validates_layout():
 
 def test_k_sliced_variants_basic_only():
     """The K-sliced 128x128 tiles (two waves along K) are planned for the Basic down and the up
-    GEMM, report four waves, and have no Stream-K form."""
+    GEMM, report four or eight waves (one or two per SIMD), and have no Stream-K form."""
     from ffn_optim_amd import _lib
     from ffn_optim_amd.host.dispatch import NotApplicable
     sliced = [v for v in _lib.variants() if v["bm"] == 128 and v["bn"] == 128 and v["stages"] >= 4]
     assert sliced, "no K-sliced variant compiled in"
     for v in sliced:
-        assert v["waves"] == 4 and v["lds_bytes"] == 160 * 1024
+        assert v["waves"] in (4, 8) and v["lds_bytes"] <= 160 * 1024
         plan = _lib.make_plan(4096, 1024, 4096, 1024, _lib.BF16, "basic", "erf", 256,
                               v["variant"], v["variant"])
         assert (plan.up_variant, plan.down_variant) == (v["variant"], v["variant"])

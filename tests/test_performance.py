@@ -52,6 +52,28 @@ def test_non_finite_timing_never_wins():
     assert best["configuration"] == {"id": "c"}
 
 
+def test_refinement_finalists_and_ranking():
+    """Tune mode re-times the distinct near-equal finalists side by side and keeps the
+    fastest by that re-timing; without one, the one-run median decides."""
+    from ffn_optim_amd.performance.tune import pick_fastest, refine_candidates
+
+    def rec(up, down, us, status="passed", **extra):
+        return dict({"status": status, "device_median_us": us,
+                     "configuration": {"up_variant": up, "down_variant": down}}, **extra)
+
+    rows = [rec(12, 10, 100.0), rec(12, 13, 101.0), rec(12, 10, 100.5), rec(0, 10, 104.9),
+            rec(12, 11, 105.1), rec(12, 1, 99.0, status="accuracy_failed"), rec(12, 3, 130.0)]
+    finalists = refine_candidates(rows)
+    assert [(r["configuration"]["up_variant"], r["configuration"]["down_variant"]) for r in finalists] \
+        == [(12, 10), (12, 13), (0, 10)]
+    assert len(refine_candidates(rows, limit=2)) == 2
+    assert pick_fastest(rows)["device_median_us"] == 100.0
+    finalists[1]["refined_median_us"] = 95.0
+    finalists[0]["refined_median_us"] = 97.0
+    assert pick_fastest(rows)["configuration"]["down_variant"] == 13
+    assert pick_fastest([rec(0, 0, 1.0, status="accuracy_failed")]) is None
+
+
 def test_checkpoint_before_interruption():
     from ffn_optim_amd.performance.tune import search
     checkpoints = []
