@@ -28,7 +28,8 @@ METRIC = "fused FFN TFLOP/s (4·M·K·H-equiv FLOPs) and % of MFMA peak, Basic v
 MFMA_PEAK_TFLOPS = 2500.0   # MI355X dense FP16/BF16 MFMA, published
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, published
 HEADLINE = "c2_aligned_bf16"
-EXTRA = ("c5_dit_bf16", "c4_decode_bf16", "c3_unaligned_fp16", "c1_smoke_fp16")
+EXTRA = ("c5_dit_bf16", "c4_decode_bf16", "c3_unaligned_fp16", "c1_smoke_fp16",
+         "c5_tp8_shard_bf16", "c4_tp8_shard_bf16")   # last two: one GPU's share of an H split over 8
 
 
 def parse_args(argv=None):

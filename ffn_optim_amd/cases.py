@@ -18,6 +18,7 @@ from .host.inputs import problem_from_shapes
 CONFIGS = Path(__file__).resolve().parent / "configs"
 BENCH_CASES = CONFIGS / "benchmark_cases.json"
 V1_CASES = CONFIGS / "v1_cases.json"
+SHARD_CASES = CONFIGS / "shard_cases.json"   # one GPU's share of an H split over 8 GPUs
 X_VIEWS = (None, "transpose12")
 
 
@@ -53,7 +54,7 @@ def case_problem(case):
 
 
 def get_case(case_id, path=None):
-    for path in ([path] if path else [BENCH_CASES, V1_CASES]):
+    for path in ([path] if path else [BENCH_CASES, V1_CASES, SHARD_CASES]):
         for case in load_cases(path):
             if case["case_id"] == case_id:
                 return case

@@ -46,6 +46,33 @@ def test_baseline_case_full(case_id, down):
 
 
 @pytest.mark.parametrize("down", ["basic", "streamk"])
+def test_tensor_parallel_shards_sum_to_full(down):
+    """An H split over 8 GPUs, run one shard after another on this GPU.  Shard g holds W1 rows
+    and W2 columns [g*H/8, (g+1)*H/8) (the shard-case shape), so its output is a partial sum
+    of the full FFN.  Each shard matches its own golden, and the FP32 sum of the eight
+    partials (the all-reduce the split needs) matches the full FFN's golden."""
+    from ffn_optim_amd import ffn
+    case = get_case("c4_decode_bf16")
+    shard = get_case("c4_tp8_shard_bf16")
+    x, w1, w2 = make_inputs(case, "cuda")
+    hs = shard["weight1_shape"][0]
+    assert hs * 8 == w1.shape[0] and shard["shape"] == case["shape"]
+    total = torch.zeros(x.shape[:-1] + (w2.shape[0],), dtype=torch.float32, device="cuda")
+    for g in range(8):
+        w1g, w2g = w1[g * hs:(g + 1) * hs], w2[:, g * hs:(g + 1) * hs]
+        part = ffn(x, w1g, w2g, down_impl=down)
+        torch.cuda.synchronize()
+        res = compare(part.cpu(), ffn_torch(x.cpu(), w1g.cpu(), w2g.cpu()))
+        say("tp8 shard", down, g, res)
+        assert res["passed"], (g, res)
+        total += part.float()
+    golden = ffn_torch(x.cpu(), w1.cpu(), w2.cpu())
+    res = compare(total.to(golden.dtype).cpu(), golden)
+    say("tp8 sum", down, res)
+    assert res["passed"], res
+
+
+@pytest.mark.parametrize("down", ["basic", "streamk"])
 def test_dit_case_sampled_rows(down):
     """Large-M case: every output row depends only on its X row, so a seeded row sample
     of the golden checks the full-size launch."""
