@@ -195,8 +195,8 @@ __device__ __forceinline__ u32x2 pack4(float a, float b, float c, float d) {
 // float64 and 1.1e-5 in FP32 evaluation, forty times below half an fp16 ulp.  (Degree 7 reaches
 // 4.6e-6 in FP32, where the rounding of x*x dominates, for two more FMAs per element: 1-3%
 // of an up GEMM.)  1/sqrt2, the factor 1/2 of h and the change to base 2 are folded into the
-// constants: one v_rcp_f32, one v_exp_f32 and about 10 full-rate VALU ops.  Like the torch
-// golden it returns NaN for z = +-inf and NaN.
+// constants: one v_rcp_f32, one v_exp_f32 and about 10 full-rate VALU ops.  NaN gives NaN,
+// as in torch; so do z = +inf (|z| * h is inf * 0; torch gives +inf) and z = -inf (torch: NaN).
 __device__ __forceinline__ float gelu_erf(float z) {
     constexpr float L2E = 1.4426950408889634f;                  // log2(e)
     const float a = __builtin_fabsf(z);
