@@ -116,7 +116,7 @@ def measure_path(case, down, steps, warmup, inputs):
     step = time_events(prepared.run, steps, warmup)
 
     def up():
-        lib.ffn_mi355x_up(ctypes.byref(plan), xs, w1s, hid, stream)
+        lib.ffn_mi355x_up(ctypes.byref(plan), xs, w1s, hid, ws, stream)
 
     def dn():
         lib.ffn_mi355x_down(ctypes.byref(plan), hid, w2s, out, ws, stream)
@@ -196,7 +196,7 @@ def counters_pass(case):
         plan = prepared.plan.native
         xs, w1s, w2s, hid, out, ws = prepared.tensors
         for _ in range(3):
-            lib.ffn_mi355x_up(ctypes.byref(plan), xs, w1s, hid, stream)
+            lib.ffn_mi355x_up(ctypes.byref(plan), xs, w1s, hid, ws, stream)
         for _ in range(3):
             lib.ffn_mi355x_down(ctypes.byref(plan), hid, w2s, out, ws, stream)
         torch.cuda.synchronize()

@@ -28,7 +28,8 @@ class PlanStruct(ctypes.Structure):
         "down_bm", "down_bn", "down_bk", "up_tiles", "up_grid",
         "down_tiles", "down_grid", "down_k_iters", "down_dp_tiles",
         "down_sk_tiles", "down_slots_per_wg")] + [("workspace_bytes", ctypes.c_size_t)] + [
-        (name, ctypes.c_int) for name in ("k", "h", "n", "ldx", "ldw1", "ldw2")]
+        (name, ctypes.c_int) for name in ("k", "h", "n", "ldx", "ldw1", "ldw2",
+                                          "up_k_iters", "up_sk_tiles", "up_slots_per_wg")]
 
     def to_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}
@@ -43,7 +44,7 @@ SIGNATURES = {
     "ffn_mi355x_workspace_bytes": (_i, [_P(PlanStruct), _P(ctypes.c_size_t)]),
     "ffn_mi355x_set_operands": (_i, [_P(PlanStruct), _i, _i, _i, _i, _i, _i]),
     "ffn_mi355x_run": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
-    "ffn_mi355x_up": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp]),
+    "ffn_mi355x_up": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp]),
     "ffn_mi355x_down": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp]),
     "ffn_mi355x_num_variants": (_i, []),
     "ffn_mi355x_variant_info": (_i, [_i, _P(_i), _P(_i), _P(_i), _P(_i), _P(_i), _P(_i)]),

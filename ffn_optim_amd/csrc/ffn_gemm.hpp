@@ -960,11 +960,12 @@ __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
 
 // Stream-K fixup, stream-ordered after ffn_gemm_kernel<..., true>: workgroup (s, b) sums the
 // FP32 partials of 32x32 accumulator block b (of every wave) of split tile s in ascending K
-// order (independent of which workgroup finished first), rounds once to the storage type and
+// order (independent of which workgroup finished first), applies the epilogue's activation
+// (none for the down GEMM, the GELU for a split up GEMM), rounds once to the storage type and
 // stores.  Each thread keeps the four 16-byte groups of its block in flight per piece, and the
 // same lane pairing as the GEMM's register epilogue (v_permlane32_swap) turns its output into
 // two 16-byte row segments.
-template <int DT, class C>
+template <int DT, class C, int EPI>
 __global__ void __launch_bounds__(C::NT) ffn_sk_reduce_kernel(GemmParams p, int blocks) {
     constexpr int TE = C::BM * C::BN;
     const int s = blockIdx.x / blocks, ji = blockIdx.x - s * blocks;
@@ -989,7 +990,9 @@ __global__ void __launch_bounds__(C::NT) ffn_sk_reduce_kernel(GemmParams p, int 
     }
     u32x2 g[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) g[q] = pack4<DT>(tot[q].x, tot[q].y, tot[q].z, tot[q].w);
+    for (int q = 0; q < 4; ++q)
+        g[q] = pack4<DT>(activate<EPI>(tot[q].x), activate<EPI>(tot[q].y), activate<EPI>(tot[q].z),
+                         activate<EPI>(tot[q].w));
     const int m = tm * C::BM + wm * C::WTM + 32 * i + (lane & 31);
     const int n0 = tn * C::BN + wn * C::WTN + 32 * j + 8 * (lane >> 5);
 #pragma unroll

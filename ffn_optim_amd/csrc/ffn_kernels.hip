@@ -36,10 +36,34 @@ void launch_gemm(const ffn::GemmParams* p, dim3 g, dim3 b, hipStream_t stream) {
         hipLaunchKernelGGL((ffn::ffn_gemm_kernel<FFN_DT, CFG, EPI, SK, false>), g, b, 0, stream, *p);
 }
 
+// Stream-K GEMM writing FP32 partials, then the fixup that sums every split tile, applies the
+// activation EPI and stores it.  Whole tiles of the GEMM leave through the plain cast, so a
+// split up GEMM (EPI a GELU) must have none.
+template <class CFG, int EPI>
+hipError_t launch_split(const ffn::GemmParams* p, dim3 g, dim3 b, hipStream_t stream) {
+    using namespace ffn;
+    if constexpr (CFG::WGK > 1) {
+        return hipErrorInvalidValue;  // a K-sliced tile has no Stream-K form
+    } else {
+        if (EPI != EPI_STORE && p->dp_tiles != 0) return hipErrorInvalidValue;
+        launch_gemm<CFG, EPI_STORE, true>(p, g, b, stream);
+        if (p->sk_tiles > 0) {
+            // one reduce workgroup per 32x32 accumulator block of each split tile: every
+            // partial load of the fixup is then in flight at once (a workgroup walking several
+            // blocks serialises their memory latencies)
+            constexpr int blocks = CFG::FN * CFG::FM;
+            hipLaunchKernelGGL((ffn_sk_reduce_kernel<FFN_DT, CFG, EPI>), dim3(p->sk_tiles * blocks), b, 0,
+                               stream, *p, blocks);
+        }
+        return hipSuccess;
+    }
+}
+
 template <class CFG>
 hipError_t launch_role(int role, const ffn::GemmParams* p, int grid, hipStream_t stream) {
     using namespace ffn;
     const dim3 g(grid), b(CFG::NT);
+    hipError_t e = hipSuccess;
     switch (role) {
         case FFN_ROLE_UP_ERF:
             launch_gemm<CFG, EPI_GELU_ERF, false>(p, g, b, stream);
@@ -51,23 +75,18 @@ hipError_t launch_role(int role, const ffn::GemmParams* p, int grid, hipStream_t
             launch_gemm<CFG, EPI_STORE, false>(p, g, b, stream);
             break;
         case FFN_ROLE_DOWN_STREAMK:
-            if constexpr (CFG::WGK > 1) {
-                return hipErrorInvalidValue;  // a K-sliced tile has no Stream-K form
-            } else {
-                launch_gemm<CFG, EPI_STORE, true>(p, g, b, stream);
-                if (p->sk_tiles > 0) {
-                    // one reduce workgroup per 32x32 accumulator block of each split tile:
-                    // every partial load of the fixup is then in flight at once (a workgroup
-                    // walking several blocks serialises their memory latencies)
-                    constexpr int blocks = CFG::FN * CFG::FM;
-                    hipLaunchKernelGGL((ffn_sk_reduce_kernel<FFN_DT, CFG>), dim3(p->sk_tiles * blocks), b,
-                                       0, stream, *p, blocks);
-                }
-            }
+            e = launch_split<CFG, EPI_STORE>(p, g, b, stream);
+            break;
+        case FFN_ROLE_UP_SPLIT_ERF:
+            e = launch_split<CFG, EPI_GELU_ERF>(p, g, b, stream);
+            break;
+        case FFN_ROLE_UP_SPLIT_RATIONAL:
+            e = launch_split<CFG, EPI_GELU_RATIONAL>(p, g, b, stream);
             break;
         default:
             return hipErrorInvalidValue;
     }
+    if (e != hipSuccess) return e;
     return hipGetLastError();
 }
 }  // namespace

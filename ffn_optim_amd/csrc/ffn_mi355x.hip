@@ -199,6 +199,34 @@ int pick_streamk(long long M, long long m_valid, long long N, long long K, int G
     return best;
 }
 
+// Split up GEMM: taken when the up's tiles would leave at least half of the workgroups idle and
+// the reduction is deep enough to split (a decode-size FFN with a narrow H, e.g. one GPU's H/8
+// share of a 16x5120 -> 13824 FFN: 27 tiles that stream W1 on 27 CUs).  Every tile must then
+// be split and shared by two or more workgroups: the GEMM stores its partials only, and the
+// fixup applies the GELU.  (A whole tile would leave the Stream-K GEMM through the plain cast.)
+// The grid cuts every tile into the largest number of equal pieces p <= G / tiles that divides
+// its iterations (none straddles two tiles), else uses all G: on that decode shard, 216
+// workgroups (8 pieces of 10 iterations) measured 12.6 us and 108 (4 of 20) 12.2 us, against
+// 14.0 us for 256 uneven pieces and 19.9 us unsplit.
+constexpr int kUpSplitMinIters = 16;
+bool split_up(const Variant& v, long long M, long long N, long long K, int G, SkShape& s) {
+    if (v.wgk > 1) return false;
+    const long long tiles = cdiv(M, v.bm) * cdiv(N, v.bn), k_iters = cdiv(K, v.bk);
+    if (tiles * 2 > G || k_iters < kUpSplitMinIters) return false;
+    long long grid = G;
+    for (long long p = G / tiles; p >= 2; --p)
+        if (k_iters % p == 0) {
+            grid = tiles * p;
+            break;
+        }
+    if (!sk_shape(v, M, N, K, (int)grid, s) || s.grid != grid || s.dp != 0 || s.sk != tiles) return false;
+    const long long kI = s.k_iters, big = (s.q + 1) * s.r;
+    auto owner = [&](long long x) { return s.q == 0 ? x : x < big ? x / (s.q + 1) : s.r + (x - big) / s.q; };
+    for (long long t = 0; t < tiles; ++t)
+        if (owner(t * kI) == owner(t * kI + kI - 1)) return false;
+    return true;
+}
+
 int group_m_for(long long tiles_m) { return (int)(tiles_m < 8 ? tiles_m : 8); }
 
 // Refill DMA addressing (GemmParams::fast_dma).  The SALU-addressed path takes the vector
@@ -337,6 +365,15 @@ int ffn_mi355x_make_plan(int m, int mp, int kp, int hp, int np, int dtype, int d
     plan->up_bm = U.bm, plan->up_bn = U.bn, plan->up_bk = U.bk;
     plan->up_tiles = (int)(cdiv(mp, U.bm) * cdiv(hp, U.bn));
     plan->up_grid = plan->up_tiles < G ? plan->up_tiles : G;
+    plan->up_k_iters = (int)cdiv(kp, U.bk);
+    size_t up_ws = 0;
+    SkShape su;
+    if (split_up(U, mp, hp, kp, G, su)) {
+        plan->up_sk_tiles = (int)su.sk;
+        plan->up_slots_per_wg = (int)su.slots;
+        plan->up_grid = (int)su.grid;
+        up_ws = (size_t)su.grid * (size_t)su.slots * (size_t)U.bm * (size_t)U.bn * 4u;
+    }
 
     // down: [mp x np], depth hp
     int dv;
@@ -388,6 +425,7 @@ int ffn_mi355x_make_plan(int m, int mp, int kp, int hp, int np, int dtype, int d
         plan->down_grid = plan->down_tiles < G ? plan->down_tiles : G;
         plan->workspace_bytes = 0;
     }
+    if (up_ws > plan->workspace_bytes) plan->workspace_bytes = up_ws;
     plan->k = kp, plan->h = hp, plan->n = np;
     plan->ldx = kp, plan->ldw1 = kp, plan->ldw2 = hp;
     return ok();
@@ -423,7 +461,8 @@ bool plan_derivation_matches(const ffn_mi355x_plan* p) {
            q.up_grid == p->up_grid && q.down_tiles == p->down_tiles && q.down_grid == p->down_grid &&
            q.down_k_iters == p->down_k_iters && q.down_dp_tiles == p->down_dp_tiles &&
            q.down_sk_tiles == p->down_sk_tiles && q.down_slots_per_wg == p->down_slots_per_wg &&
-           q.workspace_bytes == p->workspace_bytes;
+           q.workspace_bytes == p->workspace_bytes && q.up_k_iters == p->up_k_iters &&
+           q.up_sk_tiles == p->up_sk_tiles && q.up_slots_per_wg == p->up_slots_per_wg;
 }
 }  // namespace
 
@@ -436,15 +475,19 @@ int ffn_mi355x_workspace_bytes(const ffn_mi355x_plan* plan, size_t* bytes) {
 }
 
 int ffn_mi355x_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, void* hidden,
-                  void* hip_stream) {
+                  void* ws, void* hip_stream) {
     if (!valid_plan(plan)) return fail(FFN_MI355X_EINVAL, "invalid plan");
     if (!x || !w1 || !hidden) return fail(FFN_MI355X_EINVAL, "NULL device buffer");
-    if (!aligned16(x) || !aligned16(w1) || !aligned16(hidden))
+    if (!aligned16(x) || !aligned16(w1) || !aligned16(hidden) || (ws && !aligned16(ws)))
         return fail(FFN_MI355X_EINVAL, "device buffers must be 16-byte aligned");
+    const bool split = plan->up_sk_tiles > 0;
+    if (split && !ws)
+        return fail(FFN_MI355X_EINVAL, "the split up GEMM needs a workspace of %zu bytes", plan->workspace_bytes);
     int rc;
     if ((rc = check_span("x", x, span_bytes(plan->m, plan->ldx, plan->k))) != FFN_MI355X_OK ||
         (rc = check_span("w1", w1, span_bytes(plan->h, plan->ldw1, plan->k))) != FFN_MI355X_OK ||
-        (rc = check_span("hidden", hidden, span_bytes(plan->mp, plan->hp, plan->hp))) != FFN_MI355X_OK)
+        (rc = check_span("hidden", hidden, span_bytes(plan->mp, plan->hp, plan->hp))) != FFN_MI355X_OK ||
+        (split && (rc = check_span("ws", ws, plan->workspace_bytes)) != FFN_MI355X_OK))
         return rc;
     const Variant& U = kVariants[plan->up_variant];
     ffn::GemmParams gp;
@@ -455,12 +498,25 @@ int ffn_mi355x_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, vo
     gp.m_valid = plan->m, gp.n_valid = plan->h;
     gp.lda = plan->ldx, gp.ldb = plan->ldw1, gp.ldc = plan->hp;
     gp.tiles_m = (int)cdiv(plan->mp, U.bm), gp.tiles_n = (int)cdiv(plan->hp, U.bn);
-    gp.k_iters = (int)cdiv(plan->kp, U.bk);
+    gp.k_iters = plan->up_k_iters;
     gp.dp_tiles = gp.tiles_m * gp.tiles_n;
     gp.group_m = group_m_for(gp.tiles_m);
     gp.fast_dma = fast_dma_for(gp.K);
-    const int role = plan->gelu == FFN_MI355X_GELU_ERF ? FFN_ROLE_UP_ERF : FFN_ROLE_UP_RATIONAL;
-    return launch(U, plan->dtype, role, gp, plan->up_grid, hip_stream);
+    const bool erf = plan->gelu == FFN_MI355X_GELU_ERF;
+    if (split) {
+        // every tile split (no whole tiles): FP32 partials, then the fixup with the GELU
+        const long long total = (long long)plan->up_sk_tiles * plan->up_k_iters;
+        gp.dp_tiles = 0;
+        gp.sk_tiles = plan->up_sk_tiles;
+        gp.sk_q = (int)(total / plan->up_grid);
+        gp.sk_r = (int)(total % plan->up_grid);
+        gp.slots_per_wg = plan->up_slots_per_wg;
+        gp.ws = (float*)ws;
+        return launch(U, plan->dtype, erf ? FFN_ROLE_UP_SPLIT_ERF : FFN_ROLE_UP_SPLIT_RATIONAL, gp,
+                      plan->up_grid, hip_stream);
+    }
+    return launch(U, plan->dtype, erf ? FFN_ROLE_UP_ERF : FFN_ROLE_UP_RATIONAL, gp, plan->up_grid,
+                  hip_stream);
 }
 
 int ffn_mi355x_down(const ffn_mi355x_plan* plan, const void* hidden, const void* w2, void* out,
@@ -509,7 +565,7 @@ int ffn_mi355x_down(const ffn_mi355x_plan* plan, const void* hidden, const void*
 
 int ffn_mi355x_run(const ffn_mi355x_plan* plan, const void* x, const void* w1, const void* w2,
                    void* hidden, void* out, void* ws, void* hip_stream) {
-    int rc = ffn_mi355x_up(plan, x, w1, hidden, hip_stream);
+    int rc = ffn_mi355x_up(plan, x, w1, hidden, ws, hip_stream);
     if (rc != FFN_MI355X_OK) return rc;
     return ffn_mi355x_down(plan, hidden, w2, out, ws, hip_stream);
 }

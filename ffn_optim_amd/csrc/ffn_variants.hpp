@@ -36,4 +36,12 @@
 
 
 // launch roles of one variant
-enum { FFN_ROLE_UP_ERF = 0, FFN_ROLE_UP_RATIONAL = 1, FFN_ROLE_DOWN_BASIC = 2, FFN_ROLE_DOWN_STREAMK = 3 };
+// (the split up roles: every tile split along K, FP32 partials, the GELU applied in the fixup)
+enum {
+    FFN_ROLE_UP_ERF = 0,
+    FFN_ROLE_UP_RATIONAL = 1,
+    FFN_ROLE_DOWN_BASIC = 2,
+    FFN_ROLE_DOWN_STREAMK = 3,
+    FFN_ROLE_UP_SPLIT_ERF = 4,
+    FFN_ROLE_UP_SPLIT_RATIONAL = 5
+};

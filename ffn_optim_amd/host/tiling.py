@@ -41,8 +41,9 @@ class Plan:
     """Everything one FFN launch sequence needs (reference Plan, tiling.py:28-55).
 
     block_num is the persistent-workgroup count of both launches; mp/kp/hp/np are
-    the padded extents; workspace_shape is the FP32 Stream-K scratch ((1, 1) and
-    unused for the Basic down).  native is the C plan handed to the library.
+    the padded extents; workspace_shape is the FP32 scratch of the Stream-K down and of
+    a split up GEMM ((1, 1) and unused when neither splits).  native is the C plan handed
+    to the library.
     """
 
     problem: Problem
@@ -63,10 +64,12 @@ class Plan:
         return self.workspace_shape[0] * self.workspace_shape[1] * 4
 
     def schedule(self):
-        """Launch shape and Stream-K split of the down GEMM (from the native plan)."""
+        """Launch shapes, the down GEMM's Stream-K split and the up GEMM's K split (from the
+        native plan)."""
         n = self.native
-        return {"up_tiles": n.up_tiles, "up_grid": n.up_grid, "down_tiles": n.down_tiles,
-                "down_grid": n.down_grid, "down_k_iters": n.down_k_iters,
+        return {"up_tiles": n.up_tiles, "up_grid": n.up_grid, "up_k_iters": n.up_k_iters,
+                "up_sk_tiles": n.up_sk_tiles, "up_slots_per_wg": n.up_slots_per_wg,
+                "down_tiles": n.down_tiles, "down_grid": n.down_grid, "down_k_iters": n.down_k_iters,
                 "down_dp_tiles": n.down_dp_tiles, "down_sk_tiles": n.down_sk_tiles,
                 "down_slots_per_wg": n.down_slots_per_wg}
 
@@ -114,8 +117,8 @@ def make_plan(problem, selection=Selection(), block_num=DEFAULT_BLOCK_NUM, *, ge
                             -1 if down_variant is None else down_variant, m=problem.m)
     up = _tile(native.up_bm, native.up_bn, native.up_bk, native.up_variant)
     down = _tile(native.down_bm, native.down_bn, native.down_bk, native.down_variant)
-    if selection.down_impl == "streamk":
+    if native.workspace_bytes:   # Stream-K down and/or split up GEMM
         workspace = (native.workspace_bytes // 256, 64)
     else:
-        workspace = (1, 1)  # unused argument, never read by the Basic down
+        workspace = (1, 1)  # unused argument: Basic down, one workgroup per up tile
     return Plan(problem, selection, block_num, mp, kp, hp, np_, up, down, workspace, gelu, native)

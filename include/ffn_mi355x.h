@@ -64,12 +64,20 @@ typedef struct ffn_mi355x_plan {
     int down_dp_tiles;           /* tiles reduced whole by one workgroup */
     int down_sk_tiles;           /* tiles whose H-range is split over workgroups */
     int down_slots_per_wg;       /* FP32 partial-tile slots per workgroup */
-    size_t workspace_bytes;      /* FP32 partial-tile slots of the Stream-K down */
+    size_t workspace_bytes;      /* FP32 partial-tile slots of the Stream-K down and the split up */
     /* Operand layout.  ffn_mi355x_make_plan sets the padded buffers (k = kp, h = hp,
        n = np, ldx = ldw1 = kp, ldw2 = hp); ffn_mi355x_set_operands may point the plan at
        operands of their logical widths instead. */
     int k, h, n;                 /* logical K, H and N */
     int ldx, ldw1, ldw2;         /* row pitches, in elements, of X, W1 and W2 */
+    /* Split up GEMM.  When its tiles fill at most half of block_num and it is at least 16
+       iterations deep, every up tile is split along K over up_grid workgroups: FP32 partials
+       in the workspace, then a fixup that sums them in K order, applies the GELU and stores
+       hidden.  up_sk_tiles = 0: one workgroup per tile.  workspace_bytes covers both GEMMs
+       (they run one after the other on the stream). */
+    int up_k_iters;              /* BK-deep iterations along K per up tile */
+    int up_sk_tiles;             /* up tiles split along K (0 or up_tiles) */
+    int up_slots_per_wg;         /* FP32 partial-tile slots per workgroup of the split up */
 } ffn_mi355x_plan;
 
 /* Device check replacing the Ascend950/AIC checks of ops/api.py:58-66:
@@ -106,16 +114,19 @@ int ffn_mi355x_workspace_bytes(const ffn_mi355x_plan* plan, size_t* bytes);
  * dtype, then the Basic or Stream-K down GEMM writing `out` [mp,np].  Replaces
  * the single artifact(*tensors, block_num) launch of ops/api.py:43 built by
  * compile_kernel (ops/host/dispatch.py:97-116) from ops/kernel/ffn.py.
- * `ws` must hold plan->workspace_bytes (Stream-K only; may be NULL for Basic).
+ * `ws` must hold plan->workspace_bytes whenever that is nonzero (Stream-K down or
+ * split up); it may be NULL otherwise.
  * The Stream-K down is two launches: the split GEMM writing FP32 partial tiles
- * to `ws`, then the fixup summing them in ascending K order and rounding once. */
+ * to `ws`, then the fixup summing them in ascending K order and rounding once.
+ * A split up is the same two launches with the GELU applied in the fixup. */
 int ffn_mi355x_run(const ffn_mi355x_plan* plan, const void* x, const void* w1,
                    const void* w2, void* hidden, void* out, void* ws, void* hip_stream);
 
 /* Stage 1 alone: up-projection with GELU epilogue (ops/kernel/ffn.py:207-360,
- * 540-581, the cube/vector up regions of both kernels). */
+ * 540-581, the cube/vector up regions of both kernels).  `ws` holds
+ * plan->workspace_bytes when plan->up_sk_tiles > 0 (split up); it may be NULL otherwise. */
 int ffn_mi355x_up(const ffn_mi355x_plan* plan, const void* x, const void* w1,
-                  void* hidden, void* hip_stream);
+                  void* hidden, void* ws, void* hip_stream);
 
 /* Stage 2 alone: Basic (ops/kernel/ffn.py:377-529) or Stream-K
  * (ops/kernel/ffn.py:951-1423) down-projection. */

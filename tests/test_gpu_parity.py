@@ -243,8 +243,10 @@ def test_up_integer_gelu_all_variants(dtype, kp):
             plan = _lib.make_plan(mp, kp, hp, 64, _lib.BF16 if dtype == torch.bfloat16 else _lib.FP16,
                                   "basic", gelu, 256, variant, -1)
             hidden = torch.full((mp, hp), float("nan"), dtype=dtype, device="cuda")
+            ws = torch.full((max(1, plan.workspace_bytes // 4),), float("nan"), dtype=torch.float32,
+                            device="cuda")
             _lib.check(lib.ffn_mi355x_up(ctypes.byref(plan), xd.data_ptr(), w1d.data_ptr(),
-                                         hidden.data_ptr(), stream))
+                                         hidden.data_ptr(), ws.data_ptr(), stream))
             torch.cuda.synchronize()
             got = hidden.cpu()
             if gelu == "erf":

@@ -144,6 +144,60 @@ def test_streamk_schedule_exact_once_and_slots(G):
             assert n.workspace_bytes == Gs * n.down_slots_per_wg * n.down_bm * n.down_bn * 4
 
 
+@pytest.mark.parametrize("G", [8, 37, 256])
+def test_split_up_schedule_covers_once_and_shares_every_tile(G):
+    """A split up GEMM (tiles filling at most half the grid, 16 or more K-iterations) covers
+    every (tile, K-iteration) exactly once, shares every tile between two or more workgroups
+    (the fixup, not the GEMM, applies its GELU), and its slots fit the workspace (brute force).
+    Other up GEMMs keep one workgroup per tile."""
+    lib = _lib.load()
+    sliced = {v["variant"] for v in _lib.variants() if v["bm"] == v["bn"] == 128 and v["stages"] >= 4}
+    split_seen = 0
+    for (mp, kp, hp) in [(64, 5120, 1728), (64, 1024, 4096), (320, 1008, 448), (128, 256, 1024),
+                         (4096, 1024, 4096), (64, 5120, 13824)]:
+        for variant in range(lib.ffn_mi355x_num_variants()):
+            n = _lib.make_plan(mp, kp, hp, 64, _lib.BF16, "basic", "erf", G, variant, -1)
+            kI, tiles = n.up_k_iters, n.up_tiles
+            assert kI == -(-kp // n.up_bk)
+            if n.up_sk_tiles == 0:
+                assert tiles * 2 > G or kI < 16 or variant in sliced
+                assert n.up_grid == min(tiles, G)
+                continue
+            split_seen += 1
+            assert n.up_sk_tiles == tiles and tiles * 2 <= G and kI >= 16 and variant not in sliced
+            Gs = n.up_grid
+            assert tiles < Gs <= G
+            q, r = divmod(tiles * kI, Gs)
+            seen = [[0] * kI for _ in range(tiles)]
+            owners = [set() for _ in range(tiles)]
+            for v in range(Gs):
+                a, b = _sk_start(v, q, r), _sk_start(v + 1, q, r)
+                assert len({it // kI for it in range(a, b)}) <= n.up_slots_per_wg
+                for it in range(a, b):
+                    seen[it // kI][it % kI] += 1
+                    owners[it // kI].add(v)
+            assert all(c == 1 for row in seen for c in row)
+            assert all(len(o) >= 2 for o in owners)
+            assert n.workspace_bytes >= Gs * n.up_slots_per_wg * n.up_bm * n.up_bn * 4
+    assert split_seen > 0
+
+
+def test_split_up_is_planned_for_the_decode_shard_only():
+    """Of the measured workloads only the decode shard (16 x 5120 -> 1728: 27 tiles of 64x64)
+    splits its up GEMM; its Basic plan then carries a workspace for the split."""
+    from ffn_optim_amd.cases import SHARD_CASES
+    for path in (BENCH_CASES, SHARD_CASES):
+        for case in load_cases(path):
+            p = case_problem(case)
+            for down in ("basic", "streamk"):
+                plan = make_plan(p, Selection(down_impl=down), 256)
+                split = plan.native.up_sk_tiles > 0
+                assert split == (case["case_id"] == "c4_tp8_shard_bf16"), (case["case_id"], down)
+                if split:
+                    assert plan.workspace_bytes >= plan.native.workspace_bytes > 0
+                    assert plan.schedule()["up_sk_tiles"] == plan.native.up_tiles
+
+
 def test_c_abi_exports_every_declared_symbol():
     header = (REPO / "include" / "ffn_mi355x.h").read_text()
     names = set(re.findall(r"^(?:int|const char\*)\s+(ffn_mi355x_\w+)\s*\(", header, re.M))
@@ -164,7 +218,7 @@ def test_c_abi_error_codes_without_gpu():
     with pytest.raises(ValueError, match="block_num"):
         _lib.make_plan(64, 64, 64, 64, _lib.BF16, "basic", "erf", 0)
     lib = _lib.load()
-    rc = lib.ffn_mi355x_up(None, None, None, None, None)
+    rc = lib.ffn_mi355x_up(None, None, None, None, None, None)
     assert rc == _lib.EINVAL and "invalid plan" in _lib.last_error()
     info = _lib.variants()
     assert all(v["lds_bytes"] <= 160 * 1024 and v["waves"] >= 1 for v in info)
