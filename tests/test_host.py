@@ -3,6 +3,7 @@
 Restates the reference's CPU tests (validation/test_ffn.py InputTests :24-74 and
 test_selection :172-183) against this package, plus checks of the native plan.
 """
+import ctypes
 import re
 from pathlib import Path
 
@@ -180,6 +181,19 @@ def test_split_up_schedule_covers_once_and_shares_every_tile(G):
             assert all(len(o) >= 2 for o in owners)
             assert n.workspace_bytes >= Gs * n.up_slots_per_wg * n.up_bm * n.up_bn * 4
     assert split_seen > 0
+
+
+def test_split_up_without_workspace_is_refused():
+    """A plan that splits its up GEMM needs the workspace: ffn_mi355x_up and ffn_mi355x_run
+    refuse a NULL ws before touching any buffer (no device call is made)."""
+    lib = _lib.load()
+    plan = _lib.make_plan(64, 5120, 1728, 5120, _lib.BF16, "basic", "erf", 256, m=16)
+    assert plan.up_sk_tiles > 0 and plan.workspace_bytes > 0
+    fake = 1 << 40                       # aligned, never dereferenced
+    rc = lib.ffn_mi355x_up(ctypes.byref(plan), fake, fake, fake, None, None)
+    assert rc == _lib.EINVAL and "workspace" in _lib.last_error()
+    rc = lib.ffn_mi355x_run(ctypes.byref(plan), fake, fake, fake, fake, fake, None, None)
+    assert rc == _lib.EINVAL and "workspace" in _lib.last_error()
 
 
 def test_split_up_is_planned_for_the_decode_shard_only():
