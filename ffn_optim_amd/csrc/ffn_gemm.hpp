@@ -540,6 +540,11 @@ struct Engine {
                                      : DMA_ALL ? KS * NM
                                                : (KS - 1) * NM + SYNC_Q;
     static_assert(DMA_SLOTS >= 1, "at least one slot carries the refill");
+    // With two stages the stage wait (before the DMA of slot SYNC_Q of the last k-step) drains
+    // every load: a refill issued after it would land unwaited in the stage the next iteration
+    // reads.
+    static_assert(S != 2 || DMA_SLOTS <= (KS - 1) * NM + SYNC_Q,
+                  "two stages: the whole refill must be issued before the stage wait");
     // loads of the current iteration's group issued before the stage wait (after the MFMA and
     // before the DMA of slot SYNC_Q of the last k-step)
     static constexpr int DMA_BEFORE_WAIT =

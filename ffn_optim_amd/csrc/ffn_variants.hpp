@@ -10,6 +10,7 @@
 // the other's LDS and barrier waits.  Variant 12 runs the
 // 256x256 tile with eight waves (two per SIMD, 128x64 wave tiles): when every CU holds a
 // single tile, the second wave of a SIMD issues MFMAs while the first waits on LDS or DMA.
+// Its refill goes out in the first k-step of the iteration (2% faster on the DiT-size up).
 // The deep-pipeline 64-row tiles (8, 9) keep 56 KiB or more of weights in flight per CU for
 // the memory-bound small-M (decode) shapes.
 // Each variant is built for both storage types and four epilogues (GELU-erf,
@@ -29,7 +30,7 @@
     X(9, 64, 128, 64, 2, 2, 6)              \
     X(10, 128, 128, 64, 1, 2, 5, -1, 2, 2)  \
     X(11, 128, 128, 64, 1, 2, 4, -1, 2, 2)  \
-    X(12, 256, 256, 64, 2, 4, 2)            \
+    X(12, 256, 256, 64, 2, 4, 2, -1, 1)     \
     X(13, 128, 128, 64, 2, 2, 4, -1, 2, 2)
 
 #define FFN_NUM_VARIANTS 14
