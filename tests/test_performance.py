@@ -202,6 +202,15 @@ def test_runner_saves_case_preparation_interruption(tmp_path, capsys):
         runner.run()
 
 
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py --gpus N with N > 1 exits with a message before touching a device."""
+    for n in ("2", "8"):
+        proc = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", n],
+                              capture_output=True, text=True, timeout=120, cwd=ROOT)
+        assert proc.returncode != 0 and not proc.stdout.strip()
+        assert "one GPU" in proc.stdout + proc.stderr
+
+
 def test_runner_arguments_rejected():
     from ffn_optim_amd.performance.run import PerformanceRunner, parser
     for argv in (["--execute-gpu", "--dry-run"], ["--repeats", "0"], ["--write-tuned"],
