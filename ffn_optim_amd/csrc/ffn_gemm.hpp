@@ -63,8 +63,9 @@ struct GemmParams {
 };
 
 // SYNCQ_: MFMA slot of a stage's last k-step after which the stage wait + barrier is placed
-// (-1: end of the first block of B).  DMAKS_: k-steps of an iteration carrying the refill DMA
-// with two stages (-1: the first half).  WGK_: waves along K -- each wave computes its whole
+// (-1: end of the first block of B).  DMAKS_: with two stages, the k-steps at the start of an
+// iteration carrying the refill DMA (-1: the first half); with more, DMAKS_ equal to the k-steps
+// per stage spreads it over the whole iteration.  WGK_: waves along K -- each wave computes its whole
 // WTM x WTN wave tile over its own BK/WGK slice of every stage, and the WGK partial tiles are
 // summed through LDS after the main loop.
 template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int STAGES_, int SYNCQ_ = -1, int DMAKS_ = -1,
@@ -532,7 +533,8 @@ struct Engine {
     static constexpr int SYNC_Q = C::SYNCQ >= 0 ? C::SYNCQ : FM - 1;
     static_assert(SYNC_Q >= FM - 1 && SYNC_Q < NM, "the barrier may not precede the in-place B reloads");
     // Slots carrying the refill DMA.  With two stages the data is waited for at the end of the
-    // same iteration, so it goes out in the first half.  With more, it is spread over every
+    // same iteration, so it goes out in the first DMAKS k-steps (default: the first half).  With
+    // more, it is spread over every
     // slot before the stage wait, or (DMAKS == KS) over every slot of the iteration: the
     // stage wait then also allows the part of this iteration's group issued after it.
     static constexpr bool DMA_ALL = S > 2 && C::DMAKS == KS;
