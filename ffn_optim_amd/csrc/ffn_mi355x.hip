@@ -91,10 +91,11 @@ constexpr double kUnitOverhead = 2.5e-6;   // s per unit: DMA prologue latency +
 // Relative MFMA efficiency of each macro tile (measured on the FFN shapes, 256x256 = 1): the
 // fragment reads per MFMA grow as the wave tile shrinks.  A K-sliced 128x128 tile has 128x64
 // wave tiles (and pays an LDS exchange of half its partials per tile); with eight waves, two
-// per SIMD, one wave's MFMAs cover the other's waits.
+// per SIMD, one wave's MFMAs cover the other's waits.  The K-sliced 64x64 tile (64x32 wave
+// tiles, two MFMAs per k-step) is a little ahead of the plain one.
 double tile_eff(const Variant& v) {
     const int a = v.bm < v.bn ? v.bm : v.bn, b = v.bm < v.bn ? v.bn : v.bm;
-    if (v.wgk > 1) return v.nw >= 8 ? 0.9 : 0.85;
+    if (v.wgk > 1) return a >= 128 ? (v.nw >= 8 ? 0.9 : 0.85) : 0.3;
     if (a >= 256) return 1.0;
     if (a == 128 && b == 256) return 0.95;
     if (a == 128) return 0.6;
@@ -225,6 +226,20 @@ bool split_up(const Variant& v, long long M, long long N, long long K, int G, Sk
     for (long long t = 0; t < tiles; ++t)
         if (owner(t * kI) == owner(t * kI + kI - 1)) return false;
     return true;
+}
+
+// Up-GEMM tile when none is forced: every variant is priced as the plan it would get, split
+// along K (Stream-K cost, fixup included) or one workgroup per tile.
+int pick_up(long long M, long long m_valid, long long N, long long K, int G) {
+    int best = 0;
+    double best_cost = 1e300;
+    for (int i = 0; i < kNumVariants; ++i) {
+        SkShape s;
+        const double c = split_up(kVariants[i], M, N, K, G, s) ? cost_streamk(kVariants[i], s, m_valid, N, K)
+                                                                : cost_basic(kVariants[i], M, m_valid, N, K, G);
+        if (c < best_cost * 0.999) best_cost = c, best = i;
+    }
+    return best;
 }
 
 // Tile-row group of the tile order (tile_coords): consecutive tiles walk 4 tile rows column by
@@ -363,7 +378,7 @@ int ffn_mi355x_make_plan(int m, int mp, int kp, int hp, int np, int dtype, int d
     const int G = block_num;
 
     // up: [mp x hp], depth kp
-    const int uv = up_variant >= 0 ? up_variant : pick_basic(mp, m, hp, kp, G);
+    const int uv = up_variant >= 0 ? up_variant : pick_up(mp, m, hp, kp, G);
     const Variant& U = kVariants[uv];
     plan->up_variant = uv;
     plan->up_bm = U.bm, plan->up_bn = U.bn, plan->up_bk = U.bk;

@@ -12,7 +12,10 @@
 // single tile, the second wave of a SIMD issues MFMAs while the first waits on LDS or DMA.
 // Its refill goes out in the first k-step of the iteration (2% faster on the DiT-size up).
 // The deep-pipeline 64-row tiles (8, 9) keep 56 KiB or more of weights in flight per CU for
-// the memory-bound small-M (decode) shapes.
+// the memory-bound small-M (decode) shapes.  Variant 14 K-slices the 64x64 tile (64x32 wave
+// tiles over half of every stage): two MFMAs per k-step per wave instead of one, for the
+// latency-bound down GEMMs with one 64x64 tile per CU (-8 to -9% on the unaligned mid-size
+// and the decode Basic down).
 // Each variant is built for both storage types and four epilogues (GELU-erf,
 // GELU-rational, plain store, plain store + Stream-K split) in its own object.
 #pragma once
@@ -31,9 +34,10 @@
     X(10, 128, 128, 64, 1, 2, 5, -1, 2, 2)  \
     X(11, 128, 128, 64, 1, 2, 4, -1, 2, 2)  \
     X(12, 256, 256, 64, 2, 4, 2, -1, 1)     \
-    X(13, 128, 128, 64, 2, 2, 4, -1, 2, 2)
+    X(13, 128, 128, 64, 2, 2, 4, -1, 2, 2)  \
+    X(14, 64, 64, 64, 1, 2, 6, -1, 2, 2)
 
-#define FFN_NUM_VARIANTS 14
+#define FFN_NUM_VARIANTS 15
 
 
 // launch roles of one variant

@@ -152,7 +152,7 @@ def test_split_up_schedule_covers_once_and_shares_every_tile(G):
     (the fixup, not the GEMM, applies its GELU), and its slots fit the workspace (brute force).
     Other up GEMMs keep one workgroup per tile."""
     lib = _lib.load()
-    sliced = {v["variant"] for v in _lib.variants() if v["bm"] == v["bn"] == 128 and v["stages"] >= 4}
+    sliced = _k_sliced_variants()
     split_seen = 0
     for (mp, kp, hp) in [(64, 5120, 1728), (64, 1024, 4096), (320, 1008, 448), (128, 256, 1024),
                          (4096, 1024, 4096), (64, 5120, 13824)]:
@@ -332,12 +332,28 @@ def test_set_operands_validates_layout():
         assert (plan.k, plan.h, plan.n) == (1000, 3001, 999)
 
 
+def _k_sliced_variants():
+    """Variants with waves along K, found by behaviour: forced as the Stream-K down of a shape
+    every other tile splits (16 rows, 13824 deep, 5120 wide), they are refused as K-sliced."""
+    from ffn_optim_amd.host.dispatch import NotApplicable
+    out = set()
+    for v in range(_lib.load().ffn_mi355x_num_variants()):
+        try:
+            _lib.make_plan(64, 5120, 13824, 5120, _lib.BF16, "streamk", "erf", 256, 0, v, m=16)
+        except NotApplicable as exc:
+            assert "K-sliced" in str(exc), exc
+            out.add(v)
+    return out
+
+
 def test_k_sliced_variants_basic_only():
-    """The K-sliced 128x128 tiles (two waves along K) are planned for the Basic down and the up
-    GEMM, report four or eight waves (one or two per SIMD), and have no Stream-K form."""
+    """The K-sliced tiles (two waves along K) are planned for the Basic down and the up GEMM,
+    report four or eight waves (one or two per SIMD), and have no Stream-K form."""
     from ffn_optim_amd import _lib
     from ffn_optim_amd.host.dispatch import NotApplicable
-    sliced = [v for v in _lib.variants() if v["bm"] == 128 and v["bn"] == 128 and v["stages"] >= 4]
+    ids = _k_sliced_variants()
+    assert {10, 11, 13, 14} <= ids
+    sliced = [v for v in _lib.variants() if v["variant"] in ids]
     assert sliced, "no K-sliced variant compiled in"
     for v in sliced:
         assert v["waves"] in (4, 8) and v["lds_bytes"] <= 160 * 1024
