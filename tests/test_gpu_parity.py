@@ -45,6 +45,38 @@ def test_baseline_case_full(case_id, down):
     assert out.shape == golden.shape
 
 
+@pytest.mark.parametrize("case_id,down", [("c1_smoke_fp16", "basic"), ("c1_smoke_fp16", "streamk"),
+                                          ("c4_tp8_shard_bf16", "basic")])
+def test_prepared_run_replays_from_a_captured_graph(case_id, down):
+    """PreparedFFN.run() allocates, clears and synchronises nothing, so a caller can capture it in
+    a HIP graph (prepared on the capture stream, which run() checks).  Every replay, with eager
+    work on the output in between, matches the eager result bit for bit.  The decode shard's
+    plan splits its up GEMM (three launches)."""
+    case = get_case(case_id)
+    x, w1, w2 = make_inputs(case, "cuda")
+    eager = prepare_ffn(x, w1, w2, down_impl=down).run().clone()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        prepared = prepare_ffn(x, w1, w2, down_impl=down)
+        if case_id == "c4_tp8_shard_bf16":
+            assert prepared.plan.native.up_sk_tiles > 0
+        prepared.run()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            out = prepared.run()
+    torch.cuda.synchronize()
+    for replay in range(3):
+        prepared.storage[4].zero_()          # eager work on the output between replays
+        prepared.storage[3].zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        say("graph replay", case_id, down, replay)
+        assert torch.equal(out.cpu().view(torch.int16), eager.cpu().view(torch.int16)), (case_id, down, replay)
+
+
 @pytest.mark.parametrize("down", ["basic", "streamk"])
 def test_tensor_parallel_shards_sum_to_full(down):
     """An H split over 8 GPUs, run one shard after another on this GPU.  Shard g holds W1 rows
