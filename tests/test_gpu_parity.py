@@ -45,6 +45,29 @@ def test_baseline_case_full(case_id, down):
     assert out.shape == golden.shape
 
 
+@pytest.mark.parametrize("down", ["basic", "streamk"])
+@pytest.mark.parametrize("k,h,n,dtype", [(65535, 64, 64, torch.float16), (64, 65535, 64, torch.bfloat16),
+                                         (64, 64, 65535, torch.bfloat16)])
+def test_largest_dimensions(k, h, n, dtype, down):
+    """K, H or N at the input contract's maximum of 65535 (padded to 65536), 16 rows.  A 65535-deep
+    up GEMM is a single 64x64 tile, split over 256 workgroups.  Stream-K cases the reference's
+    rule refuses (no remainder tiles for 256 workgroups) must say so."""
+    from ffn_optim_amd.host.dispatch import NotApplicable
+    gen = torch.Generator().manual_seed(k + 2 * h + 3 * n)
+    x = torch.randn(16, k, generator=gen).to(dtype)
+    w1 = (torch.randn(h, k, generator=gen) * k ** -0.5).to(dtype)
+    w2 = (torch.randn(n, h, generator=gen) * h ** -0.5).to(dtype)
+    try:
+        prepared, out = run_prepared(x.cuda(), w1.cuda(), w2.cuda(), down_impl=down)
+    except NotApplicable:
+        tiles = (64 // 64) * (-(-n // 64) * 64 // 64)
+        assert down == "streamk" and tiles % 256 == 0, (k, h, n)
+        return
+    res = compare(out.cpu(), ffn_torch(x, w1, w2))
+    say("largest", k, h, n, down, prepared.plan.native.up_sk_tiles, res)
+    assert res["passed"], res
+
+
 @pytest.mark.parametrize("case_id,down", [("c1_smoke_fp16", "basic"), ("c1_smoke_fp16", "streamk"),
                                           ("c4_tp8_shard_bf16", "basic")])
 def test_prepared_run_replays_from_a_captured_graph(case_id, down):
