@@ -274,6 +274,30 @@ def test_tuning_table_roundtrip_and_planner_use(tmp_path, monkeypatch):
     assert data["schema_version"] == 1 and len(data["entries"]) == 1
 
 
+def test_committed_tuning_table_plans_every_entry():
+    """Every entry of the committed table names variants the library still accepts for its key,
+    and the measured workloads find their entry (the planner then uses those variants)."""
+    from ffn_optim_amd import _lib, tuning
+    from ffn_optim_amd.cases import BENCH_CASES, SHARD_CASES, case_problem, load_cases
+    from ffn_optim_amd.host.dispatch import Selection
+    from ffn_optim_amd.host.tiling import make_plan
+    entries = json.loads(tuning.TABLE_PATH.read_text())["entries"]
+    assert entries
+    for e in entries:
+        k = e["key"]
+        dtype = _lib.BF16 if k["dtype"] == "bfloat16" else _lib.FP16
+        plan = _lib.make_plan(k["mp"], k["kp"], k["hp"], k["np"], dtype, k["down_impl"], k["gelu"],
+                              k["block_num"], e["up_variant"], e["down_variant"], m=k["m"])
+        assert (plan.up_variant, plan.down_variant) == (e["up_variant"], e["down_variant"])
+    for path in (BENCH_CASES, SHARD_CASES):
+        for case in load_cases(path):
+            for down in ("basic", "streamk"):
+                plan = make_plan(case_problem(case), Selection(down_impl=down), 256)
+                key = tuning.make_key(plan.problem.m, plan.mp, plan.kp, plan.hp, plan.np,
+                                      plan.problem.dtype, down, "erf", 256)
+                assert tuning.lookup(key) == (plan.up.variant, plan.down.variant), (case["case_id"], down)
+
+
 def test_tuning_table_rejects_bad_entries(tmp_path):
     from ffn_optim_amd import tuning
     bad = tmp_path / "bad.json"
