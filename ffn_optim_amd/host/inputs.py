@@ -101,8 +101,9 @@ def operands_aligned(x, weight1, weight2, plan):
 def prepare_storage(x, weight1, weight2, plan, alias_aligned=False):
     """Contiguise and zero-pad into [mp,kp], [hp,kp], [np,hp]; allocate hidden, out, workspace.
 
-    Same buffers as ops/host/inputs.py:74-90; the FP32 workspace holds the Stream-K
-    partial tiles (every slot is written before it is read).  Returns the six buffers and
+    Same buffers as ops/host/inputs.py:74-90; the FP32 workspace holds the partial tiles of
+    the Stream-K down and of a split up GEMM (every slot is written before it is read).
+    Returns the six buffers and
     the operand layout (k, h, n, ldx, ldw1, ldw2) for ffn_mi355x_set_operands.
 
     With alias_aligned, every operand the kernels can read where it lies (_in_place) is
