@@ -34,7 +34,7 @@
     X(10, 128, 128, 64, 1, 2, 5, -1, 2, 2)  \
     X(11, 128, 128, 64, 1, 2, 4, -1, 2, 2)  \
     X(12, 256, 256, 64, 2, 4, 2, -1, 1)     \
-    X(13, 128, 128, 64, 2, 2, 4, -1, 2, 2)  \
+    X(13, 128, 128, 64, 2, 2, 4, 3, 2, 2)   \
     X(14, 64, 64, 64, 1, 2, 6, -1, 2, 2)
 
 #define FFN_NUM_VARIANTS 15
