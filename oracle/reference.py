@@ -1,13 +1,11 @@
 """Oracle -- TEST INFRASTRUCTURE ONLY, never part of the product path.
 
-CPU restatement of the reference's golden FFN, its error metric and its seeded
-input generator:
+CPU restatement of the reference's golden FFN and its error metric:
 
   gelu_rational  validation/reference.py:5-13   rational erf GELU (FP32)
   gelu_erf       validation/reference.py:19     F.gelu(approximate='none')
   ffn_torch      validation/reference.py:16-23  FP32 matmul -> GELU -> [stage] -> matmul -> cast
   compare        validation/test_ffn.py:6-21    mean(|o-g|/(|g|+1e-3)) < 0.05 (+ max_abs, rms)
-  make_inputs    common/cases.py:34-50          seeded randn x, w1*K^-1/2, w2*H^-1/2 (+ stride-2 view)
 
 Pinning (tests/test_oracle.py): the reference's own KATs (rational-vs-erf bound
 < 2e-5 on linspace(-10,10,10001); compare's bad-result cases), closed forms
@@ -86,37 +84,3 @@ def compare(output, golden):
                   mean_rel=(d / (b.abs() + 1e-3)).mean().item())
     result["passed"] = result["mean_rel"] < 0.05
     return result
-
-
-def make_inputs(case, device="cpu"):
-    """Deterministic inputs of one case (common/cases.py:34-50).
-
-    One CPU generator seeded with case['seed']; randn FP32 sampled in the order
-    x (scale 1), w1 (K^-1/2), w2 (H^-1/2), cast to the dtype, moved to `device`.
-    noncontiguous=True returns stride-2 views of twice-as-wide buffers.
-    """
-    import torch
-    x_shape = tuple(case["shape"])
-    h, k = case["weight1_shape"]
-    n, _ = case["weight2_shape"]
-    generator = torch.Generator(device="cpu").manual_seed(case.get("seed", 0))
-    dtype = getattr(torch, case["dtype"])
-
-    def sample(shape, scale=1.0):
-        return (torch.randn(shape, generator=generator) * scale).to(dtype).to(device)
-
-    x = sample(x_shape)
-    w1 = sample((h, k), k ** -0.5)
-    w2 = sample((n, h), h ** -0.5)
-    if case.get("noncontiguous", False):
-        def strided(t):
-            buf = torch.empty((*t.shape[:-1], t.shape[-1] * 2), dtype=t.dtype, device=t.device)
-            buf[..., ::2].copy_(t)
-            return buf[..., ::2]
-        x, w1, w2 = map(strided, (x, w1, w2))
-    return x, w1, w2
-
-
-def transposed_view(x):
-    """Same values, strides of a dim-1/dim-2 transposed buffer (the unaligned 4-D case)."""
-    return x.transpose(1, 2).contiguous().transpose(1, 2)
