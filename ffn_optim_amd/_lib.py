@@ -29,7 +29,8 @@ class PlanStruct(ctypes.Structure):
         "down_tiles", "down_grid", "down_k_iters", "down_dp_tiles",
         "down_sk_tiles", "down_slots_per_wg")] + [("workspace_bytes", ctypes.c_size_t)] + [
         (name, ctypes.c_int) for name in ("k", "h", "n", "ldx", "ldw1", "ldw2",
-                                          "up_k_iters", "up_sk_tiles", "up_slots_per_wg")]
+                                          "up_k_iters", "up_sk_tiles", "up_slots_per_wg")] + [
+        ("stamp", ctypes.c_ulonglong)]
 
     def to_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}

@@ -258,7 +258,7 @@ __device__ __forceinline__ void tile_coords(const GemmParams& p, int t, int& tm,
 
 // Split-region bookkeeping: split iteration x (0-based inside the split region) belongs to
 // workgroup sk_owner(x); workgroup v starts at sk_start(v).
-__device__ __forceinline__ int sk_owner(const GemmParams& p, int x) {
+__host__ __device__ __forceinline__ int sk_owner(const GemmParams& p, int x) {
     if (p.sk_q == 0) return x;
     const int big = (p.sk_q + 1) * p.sk_r;
     if (x < big) return x / (p.sk_q + 1);

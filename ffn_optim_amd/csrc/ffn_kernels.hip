@@ -45,7 +45,13 @@ hipError_t launch_split(const ffn::GemmParams* p, dim3 g, dim3 b, hipStream_t st
     if constexpr (CFG::WGK > 1) {
         return hipErrorInvalidValue;  // a K-sliced tile has no Stream-K form
     } else {
-        if (EPI != EPI_STORE && p->dp_tiles != 0) return hipErrorInvalidValue;
+        if constexpr (EPI != EPI_STORE) {
+            // an activation is applied by the fixup only: every tile must be split and shared
+            if (p->dp_tiles != 0) return hipErrorInvalidValue;
+            const int kI = p->k_iters;
+            for (int s = 0; s < p->sk_tiles; ++s)
+                if (sk_owner(*p, s * kI) == sk_owner(*p, s * kI + kI - 1)) return hipErrorInvalidValue;
+        }
         launch_gemm<CFG, EPI_STORE, true>(p, g, b, stream);
         if (p->sk_tiles > 0) {
             // one reduce workgroup per 32x32 accumulator block of each split tile: every

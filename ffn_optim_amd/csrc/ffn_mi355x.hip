@@ -262,10 +262,17 @@ int fast_dma_for(int k) { return k <= kFastDmaMaxK ? 1 : 0; }
 // whole 16-byte chunks, else the padded H (W2 then spans hp columns, zero past h).
 int down_depth(const ffn_mi355x_plan* p) { return p->h % 8 == 0 ? p->h : p->hp; }
 
+// Largest operand row pitch (elements).  The kernels address a macro tile's rows with 32-bit
+// buffer offsets: up to 256 rows of a pitch plus the K offset, (256 + 1) * pitch * 2 bytes,
+// must stay below 2^31, the offset that marks a zero-filled chunk.
+constexpr int kMaxPitch = 4000000;
+
+bool pitch_ok(int ld) { return ld % 8 == 0 && ld <= kMaxPitch; }
+
 bool layout_ok(const ffn_mi355x_plan* p) {
     return p->k >= 1 && p->k <= p->kp && (p->k % 8 == 0 || p->k == p->kp) && p->h >= 1 && p->h <= p->hp &&
-           p->n >= 1 && p->n <= p->np && p->ldx >= p->k && p->ldx % 8 == 0 && p->ldw1 >= p->k &&
-           p->ldw1 % 8 == 0 && p->ldw2 >= down_depth(p) && p->ldw2 % 8 == 0;
+           p->n >= 1 && p->n <= p->np && p->ldx >= p->k && pitch_ok(p->ldx) && p->ldw1 >= p->k &&
+           pitch_ok(p->ldw1) && p->ldw2 >= down_depth(p) && pitch_ok(p->ldw2);
 }
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
@@ -277,18 +284,12 @@ size_t span_bytes(long long rows, long long pitch, long long width) {
 }
 
 // [ptr, ptr + bytes) must lie inside one HIP allocation: a host pointer or a buffer too short
-// for the plan is refused before any launch instead of faulting the GPU.  Spans already checked
-// are remembered per thread, so repeated runs on the same buffers skip the lookup (a buffer
-// freed and reallocated smaller at the same address in between is not noticed).
+// for the plan is refused before any launch instead of faulting the GPU.  The runtime is asked
+// on every call (a map lookup, well under a microsecond): a cached answer would go stale when a
+// buffer is freed and a smaller one allocated at the same address.  The check sees HIP
+// allocations, not sub-blocks of a caching allocator: a span that runs past a torch tensor into
+// another block of the same segment passes.
 bool in_allocation(const void* ptr, size_t bytes) {
-    struct Seen {
-        const void* p;
-        size_t n;
-    };
-    thread_local Seen seen[16] = {};
-    thread_local int next = 0;
-    for (const Seen& e : seen)
-        if (e.p == ptr && e.n >= bytes) return true;
     hipDeviceptr_t base = nullptr;
     size_t size = 0;
     if (hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)ptr) != hipSuccess) {
@@ -296,10 +297,7 @@ bool in_allocation(const void* ptr, size_t bytes) {
         return false;
     }
     const uintptr_t b = (uintptr_t)base, q = (uintptr_t)ptr;
-    if (q < b || bytes > size || q - b > size - bytes) return false;
-    seen[next] = Seen{ptr, bytes};
-    next = (next + 1) % 16;
-    return true;
+    return q >= b && bytes <= size && q - b <= size - bytes;
 }
 
 int check_span(const char* name, const void* ptr, size_t bytes) {
@@ -308,16 +306,36 @@ int check_span(const char* name, const void* ptr, size_t bytes) {
                 name, ptr, bytes);
 }
 
-bool plan_derivation_matches(const ffn_mi355x_plan* p);
+// Check word of a plan: FNV-1a (64-bit) over every field but the stamp, seeded with a constant
+// of this library.  Fields are hashed by value, so struct padding never enters it.
+unsigned long long plan_stamp(const ffn_mi355x_plan* p) {
+    unsigned long long h = 0xcbf29ce484222325ull ^ 0x6666e6d69333535ull;
+    auto mix = [&h](unsigned long long v) {
+        for (int i = 0; i < 8; ++i) {
+            h ^= (v >> (8 * i)) & 0xffu;
+            h *= 0x100000001b3ull;
+        }
+    };
+    const int ints[] = {p->m, p->mp, p->kp, p->hp, p->np, p->dtype, p->down_impl, p->gelu, p->block_num,
+                        p->up_variant, p->down_variant, p->up_bm, p->up_bn, p->up_bk, p->down_bm, p->down_bn,
+                        p->down_bk, p->up_tiles, p->up_grid, p->down_tiles, p->down_grid, p->down_k_iters,
+                        p->down_dp_tiles, p->down_sk_tiles, p->down_slots_per_wg, p->k, p->h, p->n, p->ldx,
+                        p->ldw1, p->ldw2, p->up_k_iters, p->up_sk_tiles, p->up_slots_per_wg};
+    for (int v : ints) mix((unsigned long long)(unsigned)v);
+    mix((unsigned long long)p->workspace_bytes);
+    return h;
+}
 
 // A plan is used only as ffn_mi355x_make_plan (and ffn_mi355x_set_operands) left it: the grids,
 // tile counts, Stream-K split and workspace size it carries decide which memory the kernels
-// touch, so they are derived again from the plan's own inputs and must match.
+// touch.  Both entry points derive them and stamp the plan; a plan whose fields no longer match
+// its stamp is refused.  (The stamp catches accidental edits of a plan, not forgery.)
 bool valid_plan(const ffn_mi355x_plan* p) {
-    return p && p->m >= 1 && p->m <= p->mp && layout_ok(p) && p->up_variant >= 0 && p->up_variant < kNumVariants && p->down_variant >= 0 &&
-           p->down_variant < kNumVariants && (p->dtype == 0 || p->dtype == 1) &&
+    return p && p->stamp == plan_stamp(p) && p->m >= 1 && p->m <= p->mp && layout_ok(p) && p->up_variant >= 0 &&
+           p->up_variant < kNumVariants && p->down_variant >= 0 && p->down_variant < kNumVariants &&
+           (p->dtype == 0 || p->dtype == 1) &&
            (p->down_impl == FFN_MI355X_DOWN_BASIC || p->down_impl == FFN_MI355X_DOWN_STREAMK) &&
-           (p->gelu == 0 || p->gelu == 1) && p->block_num >= 1 && plan_derivation_matches(p);
+           (p->gelu == 0 || p->gelu == 1) && p->block_num >= 1;
 }
 
 int launch(const Variant& v, int dtype, int role, const ffn::GemmParams& gp, int grid,
@@ -450,45 +468,27 @@ int ffn_mi355x_make_plan(int m, int mp, int kp, int hp, int np, int dtype, int d
     if (up_ws > plan->workspace_bytes) plan->workspace_bytes = up_ws;
     plan->k = kp, plan->h = hp, plan->n = np;
     plan->ldx = kp, plan->ldw1 = kp, plan->ldw2 = hp;
+    if (!layout_ok(plan))
+        return fail(FFN_MI355X_EINVAL, "padded extents exceed the largest row pitch (%d elements)", kMaxPitch);
+    plan->stamp = plan_stamp(plan);
     return ok();
 }
 
 int ffn_mi355x_set_operands(ffn_mi355x_plan* plan, int k, int h, int n, int ldx, int ldw1, int ldw2) {
     if (!plan) return fail(FFN_MI355X_EINVAL, "plan must not be NULL");
+    if (!valid_plan(plan)) return fail(FFN_MI355X_EINVAL, "invalid plan");
     ffn_mi355x_plan t = *plan;
     t.k = k, t.h = h, t.n = n, t.ldx = ldx, t.ldw1 = ldw1, t.ldw2 = ldw2;
     if (!layout_ok(&t))
         return fail(FFN_MI355X_EINVAL,
                     "operand layout k=%d h=%d n=%d ldx=%d ldw1=%d ldw2=%d does not fit the plan "
                     "(kp=%d hp=%d np=%d): k a multiple of 8 or kp, pitches multiples of 8 covering "
-                    "the widths, W2 spanning hp columns when h is not a multiple of 8",
-                    k, h, n, ldx, ldw1, ldw2, plan->kp, plan->hp, plan->np);
+                    "the widths and at most %d, W2 spanning hp columns when h is not a multiple of 8",
+                    k, h, n, ldx, ldw1, ldw2, plan->kp, plan->hp, plan->np, kMaxPitch);
+    t.stamp = plan_stamp(&t);
     *plan = t;
     return ok();
 }
-
-
-}  // extern "C"
-
-namespace {
-bool plan_derivation_matches(const ffn_mi355x_plan* p) {
-    ffn_mi355x_plan q;
-    const std::string saved = g_error;
-    const int rc = ffn_mi355x_make_plan(p->m, p->mp, p->kp, p->hp, p->np, p->dtype, p->down_impl, p->gelu,
-                                        p->block_num, p->up_variant, p->down_variant, &q);
-    g_error = saved;
-    return rc == FFN_MI355X_OK && q.up_variant == p->up_variant && q.down_variant == p->down_variant &&
-           q.up_bm == p->up_bm && q.up_bn == p->up_bn && q.up_bk == p->up_bk && q.down_bm == p->down_bm &&
-           q.down_bn == p->down_bn && q.down_bk == p->down_bk && q.up_tiles == p->up_tiles &&
-           q.up_grid == p->up_grid && q.down_tiles == p->down_tiles && q.down_grid == p->down_grid &&
-           q.down_k_iters == p->down_k_iters && q.down_dp_tiles == p->down_dp_tiles &&
-           q.down_sk_tiles == p->down_sk_tiles && q.down_slots_per_wg == p->down_slots_per_wg &&
-           q.workspace_bytes == p->workspace_bytes && q.up_k_iters == p->up_k_iters &&
-           q.up_sk_tiles == p->up_sk_tiles && q.up_slots_per_wg == p->up_slots_per_wg;
-}
-}  // namespace
-
-extern "C" {
 
 int ffn_mi355x_workspace_bytes(const ffn_mi355x_plan* plan, size_t* bytes) {
     if (!plan || !bytes) return fail(FFN_MI355X_EINVAL, "NULL argument");
@@ -496,8 +496,14 @@ int ffn_mi355x_workspace_bytes(const ffn_mi355x_plan* plan, size_t* bytes) {
     return ok();
 }
 
-int ffn_mi355x_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, void* hidden,
-                  void* ws, void* hip_stream) {
+}  // extern "C"
+
+namespace {
+
+// Up GEMM of a plan.  ws_scratch: ws is this library's scratch array (its size is known, and it
+// is not a HIP allocation of its own to look up).
+int run_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, void* hidden, void* ws,
+           bool ws_scratch, void* hip_stream) {
     if (!valid_plan(plan)) return fail(FFN_MI355X_EINVAL, "invalid plan");
     if (!x || !w1 || !hidden) return fail(FFN_MI355X_EINVAL, "NULL device buffer");
     if (!aligned16(x) || !aligned16(w1) || !aligned16(hidden) || (ws && !aligned16(ws)))
@@ -509,7 +515,7 @@ int ffn_mi355x_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, vo
     if ((rc = check_span("x", x, span_bytes(plan->m, plan->ldx, plan->k))) != FFN_MI355X_OK ||
         (rc = check_span("w1", w1, span_bytes(plan->h, plan->ldw1, plan->k))) != FFN_MI355X_OK ||
         (rc = check_span("hidden", hidden, span_bytes(plan->mp, plan->hp, plan->hp))) != FFN_MI355X_OK ||
-        (split && (rc = check_span("ws", ws, plan->workspace_bytes)) != FFN_MI355X_OK))
+        (split && !ws_scratch && (rc = check_span("ws", ws, plan->workspace_bytes)) != FFN_MI355X_OK))
         return rc;
     const Variant& U = kVariants[plan->up_variant];
     ffn::GemmParams gp;
@@ -541,8 +547,9 @@ int ffn_mi355x_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, vo
                   hip_stream);
 }
 
-int ffn_mi355x_down(const ffn_mi355x_plan* plan, const void* hidden, const void* w2, void* out,
-                    void* ws, void* hip_stream) {
+// Down GEMM of a plan (ws_scratch as for run_up).
+int run_down(const ffn_mi355x_plan* plan, const void* hidden, const void* w2, void* out, void* ws,
+             bool ws_scratch, void* hip_stream) {
     if (!valid_plan(plan)) return fail(FFN_MI355X_EINVAL, "invalid plan");
     if (!hidden || !w2 || !out) return fail(FFN_MI355X_EINVAL, "NULL device buffer");
     if (!aligned16(hidden) || !aligned16(w2) || !aligned16(out) || (ws && !aligned16(ws)))
@@ -551,7 +558,7 @@ int ffn_mi355x_down(const ffn_mi355x_plan* plan, const void* hidden, const void*
     if ((rc = check_span("hidden", hidden, span_bytes(plan->m, plan->hp, down_depth(plan)))) != FFN_MI355X_OK ||
         (rc = check_span("w2", w2, span_bytes(plan->n, plan->ldw2, down_depth(plan)))) != FFN_MI355X_OK ||
         (rc = check_span("out", out, span_bytes(plan->mp, plan->np, plan->np))) != FFN_MI355X_OK ||
-        (plan->down_impl == FFN_MI355X_DOWN_STREAMK && ws &&
+        (plan->down_impl == FFN_MI355X_DOWN_STREAMK && ws && !ws_scratch &&
          (rc = check_span("ws", ws, plan->workspace_bytes)) != FFN_MI355X_OK))
         return rc;
     const Variant& D = kVariants[plan->down_variant];
@@ -585,11 +592,25 @@ int ffn_mi355x_down(const ffn_mi355x_plan* plan, const void* hidden, const void*
     return launch(D, plan->dtype, FFN_ROLE_DOWN_BASIC, gp, plan->down_grid, hip_stream);
 }
 
+}  // namespace
+
+extern "C" {
+
+int ffn_mi355x_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, void* hidden,
+                  void* ws, void* hip_stream) {
+    return run_up(plan, x, w1, hidden, ws, false, hip_stream);
+}
+
+int ffn_mi355x_down(const ffn_mi355x_plan* plan, const void* hidden, const void* w2, void* out,
+                    void* ws, void* hip_stream) {
+    return run_down(plan, hidden, w2, out, ws, false, hip_stream);
+}
+
 int ffn_mi355x_run(const ffn_mi355x_plan* plan, const void* x, const void* w1, const void* w2,
                    void* hidden, void* out, void* ws, void* hip_stream) {
-    int rc = ffn_mi355x_up(plan, x, w1, hidden, ws, hip_stream);
+    int rc = run_up(plan, x, w1, hidden, ws, false, hip_stream);
     if (rc != FFN_MI355X_OK) return rc;
-    return ffn_mi355x_down(plan, hidden, w2, out, ws, hip_stream);
+    return run_down(plan, hidden, w2, out, ws, false, hip_stream);
 }
 
 int ffn_mi355x_num_variants(void) { return kNumVariants; }

@@ -8,6 +8,7 @@ library and a load of its C entry points.
 """
 from __future__ import annotations
 
+import ctypes
 import hashlib
 from dataclasses import dataclass
 
@@ -82,10 +83,13 @@ def compile_kernel(plan):
     from .. import _lib
 
     lib = _lib.load()
-    native = plan.native
+    native = ctypes.byref(plan.native)
+    run = lib.ffn_mi355x_run
 
     def artifact(x, w1, w2, hidden, out, ws, stream):
-        _lib.check(lib.ffn_mi355x_run(native, x, w1, w2, hidden, out, ws, stream))
+        rc = run(native, x, w1, w2, hidden, out, ws, stream)
+        if rc:
+            _lib.check(rc)
 
     provenance.update(down_impl=plan.selection.down_impl,
                       entry_point=KERNEL_ENTRIES[plan.selection.down_impl],

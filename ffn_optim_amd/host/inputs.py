@@ -64,9 +64,14 @@ def problem_from_shapes(x_shape, w1_shape, w2_shape, dtype="float16", layout="li
     return Problem(x, prod(x[:-1]), k, h, n, dtype, layout)
 
 
-def validate_tensors(x, weight1, weight2, layout="linear", require_device=False):
-    """Tensor checks of ops/host/inputs.py:56-71; `require_device` asks for ROCm GPU tensors."""
+def validate_tensors(x, weight1, weight2, layout="linear", require_device=False, require_npu=None):
+    """Tensor checks of ops/host/inputs.py:56-71; `require_device` asks for ROCm GPU tensors.
+
+    require_npu is the reference's name of the same switch (ops/host/inputs.py:56), accepted
+    so that its callers run unchanged; it asks for the device this build runs on."""
     import torch
+    if require_npu is not None:
+        require_device = bool(require_npu)
 
     tensors = (x, weight1, weight2)
     if any(not isinstance(t, torch.Tensor) for t in tensors):

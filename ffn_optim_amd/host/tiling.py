@@ -35,6 +35,21 @@ class Tile:
     stages: int
     variant: int
 
+    # The reference's names for the LDS-staged macro tile (its L1 tile, ops/host/tiling.py:11-25).
+    # Its L0 tile (the cube unit's operand buffers) has no counterpart: a wave feeds the MFMA
+    # from registers, 32x32 outputs and 16 of K per instruction.
+    @property
+    def l1_tm(self):
+        return self.bm
+
+    @property
+    def l1_tn(self):
+        return self.bn
+
+    @property
+    def l1_tk(self):
+        return self.bk
+
 
 @dataclass(frozen=True)
 class Plan:
@@ -44,6 +59,12 @@ class Plan:
     the padded extents; workspace_shape is the FP32 scratch of the Stream-K down and of
     a split up GEMM ((1, 1) and unused when neither splits).  native is the C plan handed
     to the library.
+
+    workspace_shape keeps the reference's form, FP32 rows of 64 (ops/host/tiling.py:71),
+    with a row count of its own: the reference holds two 64x64 partial tiles per core,
+    (128 * block_num, 64); here a slot is one macro tile of the chosen variant (up to
+    256x256) and a workgroup holds as many slots as its split range touches tiles, so the
+    shape is (workspace_bytes / 256, 64).
     """
 
     problem: Problem

@@ -40,6 +40,22 @@ def golden(x, w1, w2, gelu="erf"):
     return y.to(x.dtype).reshape(*x.shape[:-1], w2.shape[0])
 
 
+def golden_rows(x, w1, w2, rows, gelu="erf"):
+    """golden() on a subset of the rows of X (each output row depends on its own X row only);
+    returns [len(rows), N]."""
+    m, k = x.numel() // x.shape[-1], x.shape[-1]
+    xs = x.detach().reshape(m, k)[rows.to(x.device)]
+    return golden(xs, w1, w2, gelu)
+
+
+def sample_rows(m, count=384, seed=7):
+    """A seeded sample of `count` row indices of an m-row problem (all rows when m <= count)."""
+    import torch
+    if m <= count:
+        return torch.arange(m)
+    return torch.randperm(m, generator=torch.Generator().manual_seed(seed))[:count]
+
+
 def compare(actual, expected):
     """The reference's pass/fail criterion with its diagnostics."""
     import torch

@@ -108,12 +108,40 @@ def _rows(path):
         return list(csv.DictReader(stream))
 
 
-def extract_summary(directory, kernel_name=FFN_KERNEL):
+def kernels_per_run(plan):
+    """Kernel launches of one FFN under a plan: the up GEMM, its fixup when the up GEMM is
+    split along K, the down GEMM, and its fixup for Stream-K."""
+    n = plan.native
+    return 2 + (1 if n.up_sk_tiles > 0 else 0) + (1 if n.down_sk_tiles > 0 else 0)
+
+
+def _group_runs(rows, per_run):
+    """Summed duration (us) of each FFN run in a time-ordered list of kernel dispatches.
+
+    With per_run (the launch count of one FFN, kernels_per_run) the dispatches are cut
+    into consecutive groups of that size; a trailing partial group is dropped.  Without
+    it a new run starts wherever the first kernel name recurs, which miscounts a plan
+    whose split up GEMM and Stream-K down GEMM are the same kernel instantiation."""
+    durs = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0 for r in rows]
+    if per_run:
+        return [sum(durs[i:i + per_run]) for i in range(0, len(durs) - per_run + 1, per_run)]
+    first, runs, cur = rows[0]["Kernel_Name"], [], None
+    for r, dur in zip(rows, durs):
+        if r["Kernel_Name"] == first and cur is not None:
+            runs.append(cur)
+            cur = None
+        cur = dur if cur is None else cur + dur
+    runs.append(cur)
+    return runs
+
+
+def extract_summary(directory, kernel_name=FFN_KERNEL, kernels_per_run=None):
     """Durations and counters of the FFN kernels from rocprofv3 CSV outputs under directory.
 
     task_duration_us: median over runs of the summed durations of the matching kernels of
-    one FFN, from *kernel_trace.csv (per dispatch; dispatches are grouped into runs by the
-    first matching kernel name) or, failing that, the summed AverageNs of matching rows of
+    one FFN, from *kernel_trace.csv (per dispatch; dispatches are grouped into runs of
+    kernels_per_run launches, or, when that is not given, by recurrence of the first
+    matching kernel name) or, failing that, the summed AverageNs of matching rows of
     *kernel_stats.csv.  pipeline_utilization: 'mfma_busy' per matching kernel when
     SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE were collected, as busy cycles over
     (SIMDs x GRBM_GUI_ACTIVE / XCDs) with the SIMD and XCD counts of *agent_info.csv; raw
@@ -131,14 +159,7 @@ def extract_summary(directory, kernel_name=FFN_KERNEL):
         if not rows:
             continue
         rows.sort(key=lambda r: int(r["Start_Timestamp"]))
-        first, runs, cur = rows[0]["Kernel_Name"], [], None
-        for r in rows:
-            if r["Kernel_Name"] == first and cur is not None:
-                runs.append(cur)
-                cur = None
-            dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0
-            cur = dur if cur is None else cur + dur
-        runs.append(cur)
+        runs = _group_runs(rows, kernels_per_run)
         task = _median([x for x in runs if x and x > 0])
         sources.append(str(path.relative_to(directory)))
         break

@@ -78,6 +78,11 @@ typedef struct ffn_mi355x_plan {
     int up_k_iters;              /* BK-deep iterations along K per up tile */
     int up_sk_tiles;             /* up tiles split along K (0 or up_tiles) */
     int up_slots_per_wg;         /* FP32 partial-tile slots per workgroup of the split up */
+    /* Check word over every field above, written by ffn_mi355x_make_plan and
+       ffn_mi355x_set_operands.  The run entry points refuse a plan whose fields no longer
+       match it (EINVAL "invalid plan"): its grids, tile counts and workspace size decide
+       which memory the kernels touch, so a plan is used only as the library left it. */
+    unsigned long long stamp;
 } ffn_mi355x_plan;
 
 /* Device check replacing the Ascend950/AIC checks of ops/api.py:58-66:

@@ -370,9 +370,9 @@ def test_k_sliced_variants_basic_only():
 
 
 def test_run_rejects_a_plan_whose_launch_fields_were_changed():
-    """ffn_mi355x_run / _up / _down re-derive a plan's grids, tile counts, Stream-K split and
-    workspace size from its inputs and refuse a plan that does not match (no launch is made,
-    so this runs without a GPU)."""
+    """ffn_mi355x_run / _up / _down refuse a plan whose grids, tile counts, Stream-K split,
+    workspace size or layout no longer match the stamp make_plan / set_operands wrote (no
+    launch is made, so this runs without a GPU)."""
     import ctypes
     from ffn_optim_amd import _lib
     lib = _lib.load()
@@ -386,6 +386,25 @@ def test_run_rejects_a_plan_whose_launch_fields_were_changed():
             setattr(plan, field, getattr(plan, field) + delta)
             rc = lib.ffn_mi355x_run(ctypes.byref(plan), *fake, None)
             assert rc == -1 and "invalid plan" in lib.ffn_mi355x_last_error().decode(), (down, field)
+            # nor does set_operands re-stamp a changed plan
+            rc = lib.ffn_mi355x_set_operands(ctypes.byref(plan), 1008, 3008, 1024, 1008, 1008, 3008)
+            assert rc == -1 and "invalid plan" in lib.ffn_mi355x_last_error().decode(), (down, field)
+    # the layout fields are covered too: a pitch changed behind set_operands' back
+    plan = _lib.make_plan(1024, 1008, 3008, 1024, _lib.FP16, "basic", "erf", 256)
+    plan.ldx += 8
+    assert lib.ffn_mi355x_run(ctypes.byref(plan), *fake, None) == -1
+
+
+def test_operand_pitches_are_bounded():
+    """Row pitches up to 4,000,000 elements keep a tile's 32-bit buffer offsets below the
+    2^31 zero-fill marker; a larger pitch is refused (EINVAL) instead of reading wrong rows."""
+    from ffn_optim_amd import _lib
+    plan = _lib.make_plan(1024, 1024, 1024, 1024, _lib.BF16, "basic", "erf", 256)
+    _lib.set_operands(plan, 1024, 1024, 1024, 4_000_000, 1024, 1024)
+    for pitches in ((4_000_008, 1024, 1024), (1024, 4_000_008, 1024), (1024, 1024, 4_000_008)):
+        plan = _lib.make_plan(1024, 1024, 1024, 1024, _lib.BF16, "basic", "erf", 256)
+        with pytest.raises(ValueError, match="at most 4000000"):
+            _lib.set_operands(plan, 1024, 1024, 1024, *pitches)
 
 
 def test_streamk_grid_cuts_tiles_evenly_when_it_keeps_most_workgroups():
@@ -395,3 +414,41 @@ def test_streamk_grid_cuts_tiles_evenly_when_it_keeps_most_workgroups():
     assert (plan.down_tiles, plan.down_k_iters, plan.down_grid) == (80, 216, 240)
     plan = _lib.make_plan(4096, 1024, 4096, 1024, _lib.BF16, "streamk", "erf", 256, -1, 2)
     assert (plan.down_tiles, plan.down_k_iters, plan.down_grid) == (128, 64, 256)
+
+
+def test_require_npu_is_the_reference_spelling_of_require_device():
+    """Callers written against ops/host/inputs.py:56 pass require_npu; it means "the device
+    this build runs on" and rejects CPU tensors the same way."""
+    import torch
+    from ffn_optim_amd.host.inputs import validate_tensors
+    x, a, b = torch.zeros(2, 3).half(), torch.zeros(4, 3).half(), torch.zeros(3, 4).half()
+    assert validate_tensors(x, a, b, require_npu=False).m == 2
+    with pytest.raises(ValueError, match="requires ROCm GPU tensors"):
+        validate_tensors(x, a, b, require_npu=True)
+
+
+@pytest.mark.parametrize("damage", ["missing", "corrupt"])
+def test_prepare_ffn_reports_an_unloadable_library(tmp_path, monkeypatch, damage):
+    """A missing or corrupt libffn_mi355x.so surfaces from prepare_ffn as
+    DependencyUnavailable (no fallback), before any device work (ops/host/dispatch.py:69-83)."""
+    import torch
+    from ffn_optim_amd import _lib, api
+    from ffn_optim_amd.host import inputs
+    from ffn_optim_amd.host.dispatch import DependencyUnavailable
+    lib_path = tmp_path / "libffn_mi355x.so"
+    if damage == "corrupt":
+        lib_path.write_bytes(b"\x7fELF not really a shared object")
+    monkeypatch.setattr(_lib, "LIBRARY_PATH", lib_path)
+    monkeypatch.setattr(_lib, "_lib", None)
+    # CPU tensors: let validation pass so that the library check is what fails
+    monkeypatch.setattr(api, "validate_tensors",
+                        lambda *a, **k: inputs.validate_tensors(*a, **dict(k, require_device=False)))
+    x, a, b = torch.zeros(2, 16).half(), torch.zeros(64, 16).half(), torch.zeros(8, 64).half()
+    with pytest.raises(DependencyUnavailable, match="libffn_mi355x.so"):
+        api.prepare_ffn(x, a, b)
+
+
+def test_tile_keeps_the_reference_l1_names():
+    from ffn_optim_amd.host.tiling import Tile
+    t = Tile(256, 128, 64, 4, 3, 1)
+    assert (t.l1_tm, t.l1_tn, t.l1_tk) == (256, 128, 64)
