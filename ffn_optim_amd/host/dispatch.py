@@ -83,11 +83,12 @@ def compile_kernel(plan):
     from .. import _lib
 
     lib = _lib.load()
-    native = ctypes.byref(plan.native)
+    native = plan.native
+    plan_ref = ctypes.byref(native)
     run = lib.ffn_mi355x_run
 
     def artifact(x, w1, w2, hidden, out, ws, stream):
-        rc = run(native, x, w1, w2, hidden, out, ws, stream)
+        rc = run(plan_ref, x, w1, w2, hidden, out, ws, stream)
         if rc:
             _lib.check(rc)
 

@@ -452,3 +452,19 @@ def test_tile_keeps_the_reference_l1_names():
     from ffn_optim_amd.host.tiling import Tile
     t = Tile(256, 128, 64, 4, 3, 1)
     assert (t.l1_tm, t.l1_tn, t.l1_tk) == (256, 128, 64)
+
+
+def test_compile_kernel_binds_a_plan_without_a_device():
+    """compile_kernel (ops/host/dispatch.py:97-116) loads the library and binds the plan; its
+    provenance names the entry point and the tile variants.  Binding touches no GPU."""
+    from ffn_optim_amd.host.dispatch import compile_kernel
+    from ffn_optim_amd.host.inputs import problem_from_shapes
+    from ffn_optim_amd.host.tiling import make_plan
+    for down in ("basic", "streamk"):
+        plan = make_plan(problem_from_shapes((4096, 1024), (4096, 1024), (1024, 4096), "bfloat16"),
+                         Selection("basic", down), 256)
+        artifact, prov = compile_kernel(plan)
+        assert callable(artifact)
+        assert prov["down_impl"] == down and prov["entry_point"].startswith("ffn_mi355x_run")
+        assert (prov["up_variant"], prov["down_variant"]) == (plan.up.variant, plan.down.variant)
+        assert prov["version"].startswith("ffn_mi355x gfx950")
