@@ -45,6 +45,7 @@ SIGNATURES = {
     "ffn_mi355x_workspace_bytes": (_i, [_P(PlanStruct), _P(ctypes.c_size_t)]),
     "ffn_mi355x_set_operands": (_i, [_P(PlanStruct), _i, _i, _i, _i, _i, _i]),
     "ffn_mi355x_run": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ffn_mi355x_run_noalloc": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp]),
     "ffn_mi355x_up": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp]),
     "ffn_mi355x_down": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp]),
     "ffn_mi355x_num_variants": (_i, []),

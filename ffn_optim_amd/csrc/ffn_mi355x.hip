@@ -16,6 +16,8 @@
 #include <cstdio>
 #include <cstring>
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 #include <string>
 
 #include "ffn_gemm.hpp"
@@ -592,6 +594,48 @@ int run_down(const ffn_mi355x_plan* plan, const void* hidden, const void* w2, vo
     return launch(D, plan->dtype, FFN_ROLE_DOWN_BASIC, gp, plan->down_grid, hip_stream);
 }
 
+// ---- scratch of the entry point that allocates nothing ----------------------------------
+// The FP32 partial tiles of a Stream-K down or a split up GEMM, for callers that cannot
+// allocate: device memory of this library's own code object.  Each GPU the library is loaded
+// on holds its own copy of FFN_MI355X_NOALLOC_SCRATCH_BYTES until the process ends.  In host
+// code `scratch` only names the symbol: its device address, per device, comes from
+// hipGetSymbolAddress and is what the kernels are given.
+static __device__ __align__(256) unsigned char scratch[FFN_MI355X_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch[kMaxDevices];
+std::mutex g_scratch_mutex;
+
+// Device address of `scratch` on the device of `stream`, looked up once per device with that
+// device current.
+int scratch_address(void* hip_stream, void** out) {
+    int dev = -1;
+    hipError_t e = hip_stream ? hipStreamGetDevice((hipStream_t)hip_stream, &dev) : hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(FFN_MI355X_EHIP, "device of the stream: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return fail(FFN_MI355X_EINVAL, "device %d out of range", dev);
+    void* p = g_scratch[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(g_scratch_mutex);
+        p = g_scratch[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            int cur = -1;
+            if ((e = hipGetDevice(&cur)) != hipSuccess)
+                return fail(FFN_MI355X_EHIP, "hipGetDevice: %s", hipGetErrorString(e));
+            if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess)
+                return fail(FFN_MI355X_EHIP, "hipSetDevice(%d): %s", dev, hipGetErrorString(e));
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            const hipError_t e2 = cur != dev ? hipSetDevice(cur) : hipSuccess;
+            if (e != hipSuccess || !p)
+                return fail(FFN_MI355X_EHIP, "scratch address on device %d: %s", dev, hipGetErrorString(e));
+            if (e2 != hipSuccess)
+                return fail(FFN_MI355X_EHIP, "hipSetDevice(%d): %s", cur, hipGetErrorString(e2));
+            g_scratch[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return FFN_MI355X_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -611,6 +655,24 @@ int ffn_mi355x_run(const ffn_mi355x_plan* plan, const void* x, const void* w1, c
     int rc = run_up(plan, x, w1, hidden, ws, false, hip_stream);
     if (rc != FFN_MI355X_OK) return rc;
     return run_down(plan, hidden, w2, out, ws, false, hip_stream);
+}
+
+int ffn_mi355x_run_noalloc(const ffn_mi355x_plan* plan, const void* x, const void* w1, const void* w2,
+                           void* hidden, void* out, void* hip_stream) {
+    if (!valid_plan(plan)) return fail(FFN_MI355X_EINVAL, "invalid plan");
+    if (plan->workspace_bytes > (size_t)FFN_MI355X_NOALLOC_SCRATCH_BYTES)
+        return fail(FFN_MI355X_EINVAL,
+                    "plan needs %zu bytes of workspace, more than the %zu bytes of scratch of "
+                    "ffn_mi355x_run_noalloc; run it with ffn_mi355x_run and a workspace",
+                    plan->workspace_bytes, (size_t)FFN_MI355X_NOALLOC_SCRATCH_BYTES);
+    void* ws = nullptr;
+    if (plan->workspace_bytes > 0) {
+        const int rc = scratch_address(hip_stream, &ws);
+        if (rc != FFN_MI355X_OK) return rc;
+    }
+    int rc = run_up(plan, x, w1, hidden, ws, true, hip_stream);
+    if (rc != FFN_MI355X_OK) return rc;
+    return run_down(plan, hidden, w2, out, ws, true, hip_stream);
 }
 
 int ffn_mi355x_num_variants(void) { return kNumVariants; }

@@ -127,6 +127,21 @@ int ffn_mi355x_workspace_bytes(const ffn_mi355x_plan* plan, size_t* bytes);
 int ffn_mi355x_run(const ffn_mi355x_plan* plan, const void* x, const void* w1,
                    const void* w2, void* hidden, void* out, void* ws, void* hip_stream);
 
+/* Bytes of device scratch behind ffn_mi355x_run_noalloc (per GPU, held until the process ends). */
+#define FFN_MI355X_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* ffn_mi355x_run for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * The Stream-K partial tiles (and those of a split up GEMM) go to a scratch array of the
+ * library itself, FFN_MI355X_NOALLOC_SCRATCH_BYTES per GPU; the caller passes the operands,
+ * hidden and out as for ffn_mi355x_run, and no workspace.  A plan whose workspace_bytes exceeds
+ * the scratch is refused with FFN_MI355X_EINVAL before any launch.  The call allocates and
+ * frees nothing.  Every call on one GPU shares that GPU's scratch: calls that overlap on one GPU
+ * (on different streams, or from different threads) race and must be serialised by the caller.
+ * Every partial is written before it is read within a call, so nothing needs clearing. */
+int ffn_mi355x_run_noalloc(const ffn_mi355x_plan* plan, const void* x, const void* w1,
+                           const void* w2, void* hidden, void* out, void* hip_stream);
+
 /* Stage 1 alone: up-projection with GELU epilogue (ops/kernel/ffn.py:207-360,
  * 540-581, the cube/vector up regions of both kernels).  `ws` holds
  * plan->workspace_bytes when plan->up_sk_tiles > 0 (split up); it may be NULL otherwise. */
