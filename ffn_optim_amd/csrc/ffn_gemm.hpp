@@ -60,6 +60,7 @@ struct GemmParams {
     int group_m;          // tile-order swizzle: tiles walk group_m tile-rows column by column
     int fast_dma;         // 1: launch the kernel whose interior tiles refill through the SALU-addressed DMA path
     int rev_m;            // 1: tile rows are walked last-first
+    int zero_row0;        // rows [zero_row0, M) of C lie past every tile holding data: written as zeros
 };
 
 // SYNCQ_: MFMA slot of a stage's last k-step after which the stage wait + barrier is placed
@@ -117,9 +118,11 @@ struct TileCfg {
     static_assert(BK % (16 * WGK) == 0, "every wave takes whole k-steps of a stage");
     static_assert(A_BLKS % NW == 0 && B_BLKS % NW == 0, "DMA blocks must split evenly over waves");
     static_assert(32 % (CH * R256) == 0, "fragment rows start on a swizzle period");
-    static_assert(SWZ_PERIOD <= 2, "at most two DMA offset sets");
-    static_assert(SWZ_PERIOD == 1 || (A_PW % 2 == 0 && B_PW % 2 == 0),
-                  "block parity of every DMA instruction must be known at compile time");
+    // DMA offset sets a lane keeps: one per block of the swizzle period (at least two)
+    static constexpr int NPAR = SWZ_PERIOD > 2 ? SWZ_PERIOD : 2;
+    static_assert(SWZ_PERIOD <= 4, "at most four DMA offset sets");
+    static_assert(SWZ_PERIOD == 1 || (A_PW % SWZ_PERIOD == 0 && B_PW % SWZ_PERIOD == 0),
+                  "the swizzle phase of every DMA instruction must be known at compile time");
     static_assert(LDS_ALLOC <= LDS_MAX && LDS_USE <= LDS_MAX, "gfx950 has 160 KiB of LDS per CU");
 };
 
@@ -367,8 +370,8 @@ struct Engine {
     // rows depends only on the block's parity.  a/b: byte offset of that chunk inside a block
     // at K offset 0; kk: its first K element.
     struct DmaLane {
-        uint32_t a[2], b[2];
-        int kk[2];
+        uint32_t a[C::NPAR], b[C::NPAR];
+        int kk[C::NPAR];
     };
     __device__ __forceinline__ DmaLane dma_lane(const GemmParams& p) const {
         // from an opaque lane id: the values depend only on the thread and would otherwise be
@@ -378,7 +381,7 @@ struct Engine {
         const int rl = ln / C::CH, pc = ln % C::CH;
         DmaLane d;
 #pragma unroll
-        for (int par = 0; par < 2; ++par) {
+        for (int par = 0; par < C::NPAR; ++par) {
             const int kk = (pc ^ swz_of((par % C::SWZ_PERIOD) * C::RPB + rl)) * 8;
             d.kk[par] = kk;
             d.a[par] = (uint32_t)(rl * p.lda * 2 + kk * 2);
@@ -411,7 +414,7 @@ struct Engine {
         lds_char* st = smem + stage * C::STAGE_BYTES;
         if constexpr (D < C::A_PW) {
             const int blk = wave * C::A_PW + D;
-            constexpr int par = D & 1;
+            constexpr int par = D % C::NPAR;
             const uint32_t off = L.kk[par] < t.lim
                                      ? L.a[par] + (uint32_t)blk * (uint32_t)(C::RPB * p.lda * 2) + t.k0x2
                                      : 0x80000000u;
@@ -419,7 +422,7 @@ struct Engine {
                 ra, (__attribute__((address_space(3))) void*)(st + blk * 1024), 16, (int)off, 0, 0, 0);
         } else {
             const int blk = wave * C::B_PW + (D - C::A_PW);
-            constexpr int par = (D - C::A_PW) & 1;
+            constexpr int par = (D - C::A_PW) % C::NPAR;
             const uint32_t off = L.kk[par] < t.lim
                                      ? L.b[par] + (uint32_t)blk * (uint32_t)(C::RPB * p.ldb * 2) + t.k0x2
                                      : 0x80000000u;
@@ -441,13 +444,13 @@ struct Engine {
         lds_char* st = smem + stage * C::STAGE_BYTES;
         if constexpr (D < C::A_PW) {
             const int blk = wave * C::A_PW + D;
-            constexpr int par = D & 1;
+            constexpr int par = D % C::NPAR;
             const uint32_t soff = (uint32_t)blk * (uint32_t)(C::RPB * p.lda * 2) + t.k0x2;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 ra, (__attribute__((address_space(3))) void*)(st + blk * 1024), 16, (int)L.a[par], (int)soff, 0, 0);
         } else {
             const int blk = wave * C::B_PW + (D - C::A_PW);
-            constexpr int par = (D - C::A_PW) & 1;
+            constexpr int par = (D - C::A_PW) % C::NPAR;
             const uint32_t soff = (uint32_t)blk * (uint32_t)(C::RPB * p.ldb * 2) + t.k0x2;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rb, (__attribute__((address_space(3))) void*)(st + C::A_BYTES + blk * 1024), 16, (int)L.b[par],
@@ -839,47 +842,59 @@ struct Engine {
     // contiguous 1 KiB -- the partner adds them to its own, and each slice then activates,
     // casts and stores its blocks from registers.  A sum of two FP32 terms does not depend on
     // which slice adds, so the result is bit-reproducible.  The exchange goes in phases of XB
-    // blocks per wave when the area is smaller than the blocks to send.
-    static constexpr int IH = FM / 2;                     // row blocks owned by each slice
-    static constexpr int XBLK = FN * IH;                  // blocks a wave sends
+    // blocks per wave when the area is smaller than the blocks to send.  With an odd number of
+    // row blocks (a single one: 32-row wave tiles) slice 0 owns them all, slice 1 only sends.
+    static constexpr int OWN0 = FM % 2 == 0 ? FM / 2 : FM;  // row blocks [0, OWN0) of slice 0
+    static constexpr int own_rows(int wk) { return wk == 0 ? OWN0 : FM - OWN0; }
+    static constexpr int own_base(int wk) { return wk == 0 ? 0 : OWN0; }
+    static constexpr int XMAX = FN * (OWN0 > FM - OWN0 ? OWN0 : FM - OWN0);  // most blocks a wave sends
     static constexpr int XPW = C::EPI_AVAIL / C::NW;      // exchange bytes per wave
-    static constexpr int XB = XPW / 4096 < XBLK ? XPW / 4096 : XBLK;  // blocks per phase
-    static_assert(C::WGK == 1 || (C::WGK == 2 && FM % 2 == 0 && XB >= 1),
-                  "K slicing: two slices, an even number of row blocks, room for one block per wave");
+    static constexpr int XB = XPW / 4096 < XMAX ? XPW / 4096 : XMAX;  // blocks per phase
+    static_assert(C::WGK == 1 || (C::WGK == 2 && XB >= 1),
+                  "K slicing: two slices, room for one block per wave");
 
-    template <int BASE, int B0, int B1>
+    // Block b (0-based) of the ROWS x FN blocks owned by a slice whose rows start at BASE: row
+    // block BASE + b % ROWS, column block b / ROWS.
+    template <int ROWS, int BASE, int B0, int B1>
     __device__ __forceinline__ void xsend(lds_char* area, f32x16 (&acc)[FN][FM]) const {
         if constexpr (B0 < B1) {
-            constexpr int j = B0 / IH, i = BASE + B0 % IH, sl = B0 % XB;
+            constexpr int j = B0 / ROWS, i = BASE + B0 % ROWS, sl = B0 % XB;
 #pragma unroll
             for (int q = 0; q < 4; ++q)
                 *(__attribute__((address_space(3))) f32x4*)(area + ((sl * 4 + q) * 64 + lane) * 16) =
                     f32x4{acc[j][i][4 * q], acc[j][i][4 * q + 1], acc[j][i][4 * q + 2], acc[j][i][4 * q + 3]};
-            xsend<BASE, B0 + 1, B1>(area, acc);
+            xsend<ROWS, BASE, B0 + 1, B1>(area, acc);
         }
     }
-    template <int BASE, int B0, int B1>
+    template <int ROWS, int BASE, int B0, int B1>
     __device__ __forceinline__ void xrecv(const lds_char* area, f32x16 (&acc)[FN][FM]) const {
         if constexpr (B0 < B1) {
-            constexpr int j = B0 / IH, i = BASE + B0 % IH, sl = B0 % XB;
+            constexpr int j = B0 / ROWS, i = BASE + B0 % ROWS, sl = B0 % XB;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const f32x4 v = *(const __attribute__((address_space(3))) f32x4*)(area + ((sl * 4 + q) * 64 + lane) * 16);
 #pragma unroll
                 for (int c = 0; c < 4; ++c) acc[j][i][4 * q + c] += v[c];
             }
-            xrecv<BASE, B0 + 1, B1>(area, acc);
+            xrecv<ROWS, BASE, B0 + 1, B1>(area, acc);
         }
     }
+    static constexpr int clampb(int v, int hi) { return v < hi ? v : hi; }
     template <int WK, int PH>
     __device__ __forceinline__ void xphases(f32x16 (&acc)[FN][FM]) const {
-        if constexpr (PH * XB < XBLK) {
-            constexpr int b0 = PH * XB, b1 = (PH + 1) * XB < XBLK ? (PH + 1) * XB : XBLK;
+        if constexpr (PH * XB < XMAX) {
+            // this slice sends the partner's blocks and receives its own; both lists run in
+            // phases of XB blocks (every wave passes the same barriers, also with nothing to send)
+            constexpr int PK = 1 - WK;
+            constexpr int nsend = FN * own_rows(PK), nrecv = FN * own_rows(WK);
+            constexpr int b0 = PH * XB, b1 = (PH + 1) * XB;
             const int partner = wave + (WK == 0 ? 1 : -1) * C::WGM * C::WGN;
             if constexpr (PH > 0) barrier();  // the partner has read the previous phase
-            xsend<(1 - WK) * IH, b0, b1>(smem + C::EPI_OFF + wave * XPW, acc);
+            xsend<(own_rows(PK) > 0 ? own_rows(PK) : 1), own_base(PK), clampb(b0, nsend), clampb(b1, nsend)>(
+                smem + C::EPI_OFF + wave * XPW, acc);
             barrier();
-            xrecv<WK * IH, b0, b1>(smem + C::EPI_OFF + partner * XPW, acc);
+            xrecv<(own_rows(WK) > 0 ? own_rows(WK) : 1), own_base(WK), clampb(b0, nrecv), clampb(b1, nrecv)>(
+                smem + C::EPI_OFF + partner * XPW, acc);
             xphases<WK, PH + 1>(acc);
         }
     }
@@ -892,7 +907,7 @@ struct Engine {
         else wait_vmcnt<0>();
         barrier();
         xphases<WK, 0>(acc);
-        store_tile_regs<EPI, WK * IH, (WK + 1) * IH>(p, u, acc);
+        store_tile_regs<EPI, own_base(WK), own_base(WK) + own_rows(WK)>(p, u, acc);
     }
     template <int EPI>
     __device__ __forceinline__ void store_sliced(const GemmParams& p, const Unit& u, bool next,
@@ -902,21 +917,41 @@ struct Engine {
         else store_sliced_as<EPI, 1>(p, u, next, acc);
     }
 
-    // FP32 partial tile in the accumulator's own register order: group (j, i, q) of thread
-    // tid lives at ((j*FM + i)*4 + q)*NT + tid (16-byte units), so every store is coalesced.
+    // FP32 partial tile in the accumulator's own register order: group (j, i, q) of logical
+    // thread t lives at ((j*FM + i)*4 + q)*NTL + t (16-byte units), so every store is coalesced.
+    // t is the thread's index among the WGM x WGN waves of one K slice, NTL their thread count:
+    // a K-sliced tile first sums its slices (the exchange above) and each slice then writes the
+    // row blocks [I0, I1) it owns.
+    static constexpr int NTL = C::NT / C::WGK;
+    template <int I0 = 0, int I1 = FM>
     __device__ __forceinline__ void store_partial(float* slot, f32x16 (&acc)[FN][FM]) const {
+        const int t = tid - wk * NTL;
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
-            for (int i = 0; i < FM; ++i)
+            for (int i = I0; i < I1; ++i)
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int idx = (j * FM + i) * 4 + q;
                     const f32x4 v = {acc[j][i][4 * q], acc[j][i][4 * q + 1], acc[j][i][4 * q + 2],
                                      acc[j][i][4 * q + 3]};
-                    *(f32x4*)(slot + ((size_t)idx * NT + tid) * 4) = v;
+                    *(f32x4*)(slot + ((size_t)idx * NTL + t) * 4) = v;
                     if (q == 3) __builtin_amdgcn_sched_barrier(0);
                 }
+    }
+    template <int WK>
+    __device__ __forceinline__ void store_partial_sliced_as(float* slot, bool next, f32x16 (&acc)[FN][FM]) {
+        if (next) wait_vmcnt<C::LOADS * (S - 1)>();
+        else wait_vmcnt<0>();
+        barrier();
+        xphases<WK, 0>(acc);
+        store_partial<own_base(WK), own_base(WK) + own_rows(WK)>(slot, acc);
+    }
+    // Partial of a Stream-K piece of a K-sliced tile: the slices are summed first (as for a whole
+    // tile), then each slice stores the blocks it owns.
+    __device__ __forceinline__ void store_partial_sliced(float* slot, bool next, f32x16 (&acc)[FN][FM]) {
+        if (wk == 0) store_partial_sliced_as<0>(slot, next, acc);
+        else store_partial_sliced_as<1>(slot, next, acc);
     }
 };
 
@@ -931,8 +966,7 @@ __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
     // store_partial, stores its whole tiles from registers too: the staging registers would
     // push it past 256 VGPRs.
     // A K-sliced tile exchanges its partial sums through the free stage(s) and stores from
-    // registers (it has no Stream-K form: its split pieces would need the exchange first).
-    static_assert(C::WGK == 1 || !SK, "no Stream-K form of a K-sliced tile");
+    // registers; its Stream-K pieces exchange first and then store their FP32 partials.
     constexpr bool EPI_IN_REGS = EPI != EPI_STORE || SK;
     constexpr int SMEM = C::WGK > 1 ? C::LDS_USE : EPI_IN_REGS ? C::LDS_BYTES : C::LDS_ALLOC;
     __shared__ __attribute__((aligned(1024))) char smem_raw[SMEM];
@@ -945,6 +979,16 @@ __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
     // consecutive virtual ids (which take neighbouring tiles) share one XCD's L2.
     const int v = ((G & 7) == 0) ? (g & 7) * (G >> 3) + (g >> 3) : g;
 
+    // Output rows past the last tile row that holds data (zero padding of a small-M problem) are
+    // not computed: every workgroup writes its share of them as zeros, ahead of its first unit.
+    if (p.zero_row0 < p.M) {
+        const int cpr = p.N / 8;  // 16-byte chunks per row
+        const long long total = (long long)(p.M - p.zero_row0) * cpr;
+        for (long long i = (long long)g * C::NT + threadIdx.x; i < total; i += (long long)G * C::NT) {
+            const long long r = p.zero_row0 + i / cpr, c = i % cpr;
+            *(u32x4*)((char*)p.c + ((size_t)r * (size_t)p.ldc + (size_t)c * 8) * 2) = u32x4{0u, 0u, 0u, 0u};
+        }
+    }
     UnitWalker<SK> walk(p, v, G);
     Unit u = walk.next(p);
     if (!u.valid) return;
@@ -952,9 +996,11 @@ __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
     while (true) {
         const Unit nx = walk.next(p);
         eng.template mainloop<FASTK>(p, u, nx, acc);
-        if (SK && u.split >= 0)
-            eng.store_partial(sk_slot(p, v, u.local, C::BM * C::BN), acc);
-        else if constexpr (C::WGK > 1)
+        if (SK && u.split >= 0) {
+            float* slot = sk_slot(p, v, u.local, C::BM * C::BN);
+            if constexpr (C::WGK > 1) eng.store_partial_sliced(slot, nx.valid, acc);
+            else eng.store_partial(slot, acc);
+        } else if constexpr (C::WGK > 1)
             eng.template store_sliced<EPI>(p, u, nx.valid, acc);
         else if constexpr (EPI_IN_REGS)
             eng.template store_tile_regs<EPI>(p, u, acc);
@@ -981,6 +1027,9 @@ __global__ void __launch_bounds__(C::NT) ffn_sk_reduce_kernel(GemmParams p, int 
     if (first == last) return;  // stored whole by its only contributor
     int tm, tn;
     tile_coords(p, p.dp_tiles + s, tm, tn);
+    // launched with the threads of one K slice (NTL = NT / WGK): thread t is the partial
+    // layout's logical thread (Engine::store_partial)
+    constexpr int NTL = C::NT / C::WGK;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave % C::WGM, wn = wave / C::WGM;
     const int j = ji / C::FM, i = ji - j * C::FM;
@@ -988,12 +1037,12 @@ __global__ void __launch_bounds__(C::NT) ffn_sk_reduce_kernel(GemmParams p, int 
     {
         const float* slot = sk_slot(p, first, s - sk_start(p, first) / kI, TE);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) tot[q] = *(const f32x4*)(slot + ((size_t)(ji * 4 + q) * C::NT + tid) * 4);
+        for (int q = 0; q < 4; ++q) tot[q] = *(const f32x4*)(slot + ((size_t)(ji * 4 + q) * NTL + tid) * 4);
     }
     for (int w = first + 1; w <= last; ++w) {
         const float* slot = sk_slot(p, w, s - sk_start(p, w) / kI, TE);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) tot[q] += *(const f32x4*)(slot + ((size_t)(ji * 4 + q) * C::NT + tid) * 4);
+        for (int q = 0; q < 4; ++q) tot[q] += *(const f32x4*)(slot + ((size_t)(ji * 4 + q) * NTL + tid) * 4);
     }
     u32x2 g[4];
 #pragma unroll

@@ -37,32 +37,29 @@ void launch_gemm(const ffn::GemmParams* p, dim3 g, dim3 b, hipStream_t stream) {
 }
 
 // Stream-K GEMM writing FP32 partials, then the fixup that sums every split tile, applies the
-// activation EPI and stores it.  Whole tiles of the GEMM leave through the plain cast, so a
+// activation EPI and stores it (K-sliced tiles included: their slices are summed before a
+// partial is written).  Whole tiles of the GEMM leave through the plain cast, so a
 // split up GEMM (EPI a GELU) must have none.
 template <class CFG, int EPI>
 hipError_t launch_split(const ffn::GemmParams* p, dim3 g, dim3 b, hipStream_t stream) {
     using namespace ffn;
-    if constexpr (CFG::WGK > 1) {
-        return hipErrorInvalidValue;  // a K-sliced tile has no Stream-K form
-    } else {
-        if constexpr (EPI != EPI_STORE) {
-            // an activation is applied by the fixup only: every tile must be split and shared
-            if (p->dp_tiles != 0) return hipErrorInvalidValue;
-            const int kI = p->k_iters;
-            for (int s = 0; s < p->sk_tiles; ++s)
-                if (sk_owner(*p, s * kI) == sk_owner(*p, s * kI + kI - 1)) return hipErrorInvalidValue;
-        }
-        launch_gemm<CFG, EPI_STORE, true>(p, g, b, stream);
-        if (p->sk_tiles > 0) {
-            // one reduce workgroup per 32x32 accumulator block of each split tile: every
-            // partial load of the fixup is then in flight at once (a workgroup walking several
-            // blocks serialises their memory latencies)
-            constexpr int blocks = CFG::FN * CFG::FM;
-            hipLaunchKernelGGL((ffn_sk_reduce_kernel<FFN_DT, CFG, EPI>), dim3(p->sk_tiles * blocks), b, 0,
-                               stream, *p, blocks);
-        }
-        return hipSuccess;
+    if constexpr (EPI != EPI_STORE) {
+        // an activation is applied by the fixup only: every tile must be split and shared
+        if (p->dp_tiles != 0) return hipErrorInvalidValue;
+        const int kI = p->k_iters;
+        for (int s = 0; s < p->sk_tiles; ++s)
+            if (sk_owner(*p, s * kI) == sk_owner(*p, s * kI + kI - 1)) return hipErrorInvalidValue;
     }
+    launch_gemm<CFG, EPI_STORE, true>(p, g, b, stream);
+    if (p->sk_tiles > 0) {
+        // one reduce workgroup per 32x32 accumulator block of each split tile: every partial
+        // load of the fixup is then in flight at once (a workgroup walking several blocks
+        // serialises their memory latencies); the threads of one K slice cover the tile
+        constexpr int blocks = CFG::FN * CFG::FM;
+        hipLaunchKernelGGL((ffn_sk_reduce_kernel<FFN_DT, CFG, EPI>), dim3(p->sk_tiles * blocks),
+                           dim3(CFG::NT / CFG::WGK), 0, stream, *p, blocks);
+    }
+    return hipSuccess;
 }
 
 template <class CFG>

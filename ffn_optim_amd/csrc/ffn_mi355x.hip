@@ -119,7 +119,8 @@ long long rows_in_tile(const Variant& v, long long m_valid) { return std::min<lo
 
 // Estimated seconds of a data-parallel GEMM [M x N] (m_valid data rows), depth K.
 double cost_basic(const Variant& v, long long M, long long m_valid, long long N, long long K, int G) {
-    const long long T = cdiv(M, v.bm) * cdiv(N, v.bn);
+    (void)M;
+    const long long T = cdiv(m_valid, v.bm) * cdiv(N, v.bn);
     const long long waves = cdiv(T, G);
     const double t = (double)waves * ((double)cdiv(K, v.bk) * iter_time(v, rows_in_tile(v, m_valid)) +
                                       kUnitOverhead);
@@ -149,8 +150,10 @@ long long sk_grid(long long tiles, long long k_iters, int G) {
     return G;
 }
 
-bool sk_shape(const Variant& v, long long M, long long N, long long K, int block_num, SkShape& s) {
-    s.tiles = cdiv(M, v.bm) * cdiv(N, v.bn);
+// Tiles of a GEMM whose rows [m_valid, M) are zero padding: only tile rows holding data are
+// computed (the kernel zero-fills the rows past them).
+bool sk_shape(const Variant& v, long long m_valid, long long N, long long K, int block_num, SkShape& s) {
+    s.tiles = cdiv(m_valid, v.bm) * cdiv(N, v.bn);
     s.k_iters = cdiv(K, v.bk);
     const long long G = sk_grid(s.tiles, s.k_iters, block_num);
     s.grid = G;
@@ -198,7 +201,7 @@ int pick_streamk(long long M, long long m_valid, long long N, long long K, int G
     double best_cost = 1e300;
     for (int i = 0; i < kNumVariants; ++i) {
         SkShape s;
-        if (kVariants[i].wgk > 1 || !sk_shape(kVariants[i], M, N, K, G, s)) continue;
+        if (!sk_shape(kVariants[i], m_valid, N, K, G, s)) continue;
         const double c = cost_streamk(kVariants[i], s, m_valid, N, K);
         if (c < best_cost * 0.999) best_cost = c, best = i;
     }
@@ -215,9 +218,8 @@ int pick_streamk(long long M, long long m_valid, long long N, long long K, int G
 // workgroups (8 pieces of 10 iterations) measured 12.6 us and 108 (4 of 20) 12.2 us, against
 // 14.0 us for 256 uneven pieces and 19.9 us unsplit.
 constexpr int kUpSplitMinIters = 16;
-bool split_up(const Variant& v, long long M, long long N, long long K, int G, SkShape& s) {
-    if (v.wgk > 1) return false;
-    const long long tiles = cdiv(M, v.bm) * cdiv(N, v.bn), k_iters = cdiv(K, v.bk);
+bool split_up(const Variant& v, long long m_valid, long long N, long long K, int G, SkShape& s) {
+    const long long tiles = cdiv(m_valid, v.bm) * cdiv(N, v.bn), k_iters = cdiv(K, v.bk);
     if (tiles * 2 > G || k_iters < kUpSplitMinIters) return false;
     long long grid = G;
     for (long long p = G / tiles; p >= 2; --p)
@@ -225,7 +227,7 @@ bool split_up(const Variant& v, long long M, long long N, long long K, int G, Sk
             grid = tiles * p;
             break;
         }
-    if (!sk_shape(v, M, N, K, (int)grid, s) || s.grid != grid || s.dp != 0 || s.sk != tiles) return false;
+    if (!sk_shape(v, m_valid, N, K, (int)grid, s) || s.grid != grid || s.dp != 0 || s.sk != tiles) return false;
     const long long kI = s.k_iters, big = (s.q + 1) * s.r;
     auto owner = [&](long long x) { return s.q == 0 ? x : x < big ? x / (s.q + 1) : s.r + (x - big) / s.q; };
     for (long long t = 0; t < tiles; ++t)
@@ -240,7 +242,7 @@ int pick_up(long long M, long long m_valid, long long N, long long K, int G) {
     double best_cost = 1e300;
     for (int i = 0; i < kNumVariants; ++i) {
         SkShape s;
-        const double c = split_up(kVariants[i], M, N, K, G, s) ? cost_streamk(kVariants[i], s, m_valid, N, K)
+        const double c = split_up(kVariants[i], m_valid, N, K, G, s) ? cost_streamk(kVariants[i], s, m_valid, N, K)
                                                                 : cost_basic(kVariants[i], M, m_valid, N, K, G);
         if (c < best_cost * 0.999) best_cost = c, best = i;
     }
@@ -405,12 +407,12 @@ int ffn_mi355x_make_plan(int m, int mp, int kp, int hp, int np, int dtype, int d
     const Variant& U = kVariants[uv];
     plan->up_variant = uv;
     plan->up_bm = U.bm, plan->up_bn = U.bn, plan->up_bk = U.bk;
-    plan->up_tiles = (int)(cdiv(mp, U.bm) * cdiv(hp, U.bn));
+    plan->up_tiles = (int)(cdiv(m, U.bm) * cdiv(hp, U.bn));
     plan->up_grid = plan->up_tiles < G ? plan->up_tiles : G;
     plan->up_k_iters = (int)cdiv(kp, U.bk);
     size_t up_ws = 0;
     SkShape su;
-    if (split_up(U, mp, hp, kp, G, su)) {
+    if (split_up(U, m, hp, kp, G, su)) {
         plan->up_sk_tiles = (int)su.sk;
         plan->up_slots_per_wg = (int)su.slots;
         plan->up_grid = (int)su.grid;
@@ -422,11 +424,7 @@ int ffn_mi355x_make_plan(int m, int mp, int kp, int hp, int np, int dtype, int d
     if (down_impl == FFN_MI355X_DOWN_STREAMK) {
         if (down_variant >= 0) {
             SkShape s;
-            if (kVariants[down_variant].wgk > 1)
-                return fail(FFN_MI355X_ENOT_APPLICABLE,
-                            "Stream-K candidate: tile variant %d is K-sliced and has no Stream-K form",
-                            down_variant);
-            if (!sk_shape(kVariants[down_variant], mp, np, hp, G, s)) {
+            if (!sk_shape(kVariants[down_variant], m, np, hp, G, s)) {
                 if (s.k_iters < 2)
                     return fail(FFN_MI355X_ENOT_APPLICABLE,
                                 "Stream-K candidate requires at least two K tiles along H");
@@ -452,11 +450,11 @@ int ffn_mi355x_make_plan(int m, int mp, int kp, int hp, int np, int dtype, int d
     const Variant& D = kVariants[dv];
     plan->down_variant = dv;
     plan->down_bm = D.bm, plan->down_bn = D.bn, plan->down_bk = D.bk;
-    plan->down_tiles = (int)(cdiv(mp, D.bm) * cdiv(np, D.bn));
+    plan->down_tiles = (int)(cdiv(m, D.bm) * cdiv(np, D.bn));
     plan->down_k_iters = (int)cdiv(hp, D.bk);
     if (down_impl == FFN_MI355X_DOWN_STREAMK) {
         SkShape s;
-        sk_shape(D, mp, np, hp, G, s);
+        sk_shape(D, m, np, hp, G, s);
         plan->down_dp_tiles = (int)s.dp;
         plan->down_sk_tiles = (int)s.sk;
         plan->down_slots_per_wg = (int)s.slots;
@@ -527,7 +525,8 @@ int run_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, void* hid
     gp.M = plan->mp, gp.N = plan->hp, gp.K = plan->k;
     gp.m_valid = plan->m, gp.n_valid = plan->h;
     gp.lda = plan->ldx, gp.ldb = plan->ldw1, gp.ldc = plan->hp;
-    gp.tiles_m = (int)cdiv(plan->mp, U.bm), gp.tiles_n = (int)cdiv(plan->hp, U.bn);
+    gp.tiles_m = (int)cdiv(plan->m, U.bm), gp.tiles_n = (int)cdiv(plan->hp, U.bn);
+    gp.zero_row0 = (int)std::min<long long>(plan->mp, (long long)gp.tiles_m * U.bm);
     gp.k_iters = plan->up_k_iters;
     gp.dp_tiles = gp.tiles_m * gp.tiles_n;
     gp.group_m = group_m_for(gp.tiles_m);
@@ -570,7 +569,8 @@ int run_down(const ffn_mi355x_plan* plan, const void* hidden, const void* w2, vo
     gp.M = plan->mp, gp.N = plan->np, gp.K = down_depth(plan);
     gp.m_valid = plan->m, gp.n_valid = plan->n;
     gp.lda = plan->hp, gp.ldb = plan->ldw2, gp.ldc = plan->np;
-    gp.tiles_m = (int)cdiv(plan->mp, D.bm), gp.tiles_n = (int)cdiv(plan->np, D.bn);
+    gp.tiles_m = (int)cdiv(plan->m, D.bm), gp.tiles_n = (int)cdiv(plan->np, D.bn);
+    gp.zero_row0 = (int)std::min<long long>(plan->mp, (long long)gp.tiles_m * D.bm);
     gp.k_iters = plan->down_k_iters;
     gp.group_m = group_m_for(gp.tiles_m);
     gp.fast_dma = fast_dma_for(gp.K);

@@ -35,9 +35,11 @@
     X(11, 128, 128, 64, 1, 2, 4, -1, 2, 2)  \
     X(12, 256, 256, 64, 2, 4, 2, -1, 1)     \
     X(13, 128, 128, 64, 2, 2, 4, 3, 2, 2)   \
-    X(14, 64, 64, 64, 1, 2, 6, -1, 2, 2)
+    X(14, 64, 64, 64, 1, 2, 6, -1, 2, 2)    \
+    X(15, 32, 32, 128, 1, 1, 8, -1, 4, 2)   \
+    X(16, 64, 64, 128, 1, 2, 5, -1, 4, 2)
 
-#define FFN_NUM_VARIANTS 15
+#define FFN_NUM_VARIANTS 17
 
 
 // launch roles of one variant

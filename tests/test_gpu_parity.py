@@ -23,6 +23,36 @@ def say(*args):
     print("[gpu-test]", *args, flush=True)
 
 
+# Tripwires well inside the reference criterion (mean_rel < 0.05).  Against the unstaged golden
+# (FP32 hidden) the error is set by the hidden activation's own rounding to the input dtype:
+# measured ~8.5e-4 (fp16) and ~6.9e-3 (bf16) on the benchmark workloads.  Against the staged
+# golden (hidden rounded to the input dtype, as the kernels store it) only the FP32 summation
+# order and the erf approximation remain: measured at most 2.4e-4.
+UNSTAGED_BOUND = {torch.float16: 2e-3, torch.bfloat16: 1.2e-2}
+STAGED_BOUND = 1e-3
+
+
+def assert_parity(out, x, w1, w2, rows=None, rational=False, tag=""):
+    """out against the reference criterion and both tripwires; rows: check only these rows of
+    X (each output row depends on its own X row)."""
+    xc, w1c, w2c = x.cpu(), w1.cpu(), w2.cpu()
+    if rows is None:
+        got = out.cpu()
+        golden = ffn_torch(xc, w1c, w2c, rational=rational)
+        staged = ffn_torch(xc, w1c, w2c, staged=True, rational=rational)
+    else:
+        m = x.numel() // x.shape[-1]
+        got = out.reshape(m, -1)[rows.to(out.device)].cpu()
+        golden = ffn_rows(xc, w1c, w2c, rows, rational=rational)
+        staged = ffn_rows(xc, w1c, w2c, rows, staged=True, rational=rational)
+    res, res_staged = compare(got, golden), compare(got, staged)
+    say(tag, "unstaged", res, "staged", res_staged)
+    assert res["passed"], res
+    assert res["mean_rel"] <= UNSTAGED_BOUND[x.dtype], res
+    assert res_staged["mean_rel"] <= STAGED_BOUND, res_staged
+    return res
+
+
 def run_prepared(x, w1, w2, **kw):
     prepared = prepare_ffn(x, w1, w2, **kw)
     out = prepared.run()
@@ -38,11 +68,8 @@ def test_baseline_case_full(case_id, down):
     say(case_id, down)
     x, w1, w2 = make_inputs(case, "cuda")
     prepared, out = run_prepared(x, w1, w2, down_impl=down)
-    golden = ffn_torch(x.cpu(), w1.cpu(), w2.cpu())
-    res = compare(out.cpu(), golden)
-    say(case_id, down, prepared.plan.up, prepared.plan.down, res)
-    assert res["passed"], res
-    assert out.shape == golden.shape
+    assert_parity(out, x, w1, w2, tag=f"{case_id} {down} v{prepared.plan.up.variant}/v{prepared.plan.down.variant}")
+    assert out.shape == tuple(case["shape"][:-1]) + (case["weight2_shape"][0],)
 
 
 @pytest.mark.parametrize("down", ["basic", "streamk"])
@@ -137,11 +164,7 @@ def test_dit_case_sampled_rows(down):
     prepared, out = run_prepared(x, w1, w2, down_impl=down)
     m = x.numel() // x.shape[-1]
     rows = torch.randperm(m, generator=torch.Generator().manual_seed(7))[:384]
-    golden = ffn_rows(x.cpu(), w1.cpu(), w2.cpu(), rows)
-    got = out.reshape(m, -1)[rows.cuda()].cpu()
-    res = compare(got, golden)
-    say("c5", down, res)
-    assert res["passed"], res
+    assert_parity(out, x, w1, w2, rows=rows, tag=f"c5 {down}")
 
 
 @pytest.mark.parametrize("down", ["basic", "streamk"])
@@ -154,11 +177,7 @@ def test_reference_smoke_cases(case, down):
     except ValueError as exc:  # NotApplicable is a ValueError
         assert down == "streamk", exc
         pytest.skip(f"streamk not applicable: {exc}")
-    golden = ffn_torch(x.cpu(), w1.cpu(), w2.cpu())
-    staged = ffn_torch(x.cpu(), w1.cpu(), w2.cpu(), staged=True)
-    res, res_staged = compare(out.cpu(), golden), compare(out.cpu(), staged)
-    say(case["case_id"], down, res, res_staged)
-    assert res["passed"] and res_staged["passed"]
+    assert_parity(out, x, w1, w2, tag=f"{case['case_id']} {down}")
     assert out.shape == tuple(case["shape"][:-1]) + (case["weight2_shape"][0],)
 
 
@@ -184,10 +203,7 @@ def test_rational_gelu_option(down):
     case = get_case("c2_aligned_bf16")
     x, w1, w2 = make_inputs(case, "cuda")
     _, out = run_prepared(x, w1, w2, down_impl=down, gelu="rational")
-    golden = ffn_torch(x.cpu(), w1.cpu(), w2.cpu(), staged=True, rational=True)
-    res = compare(out.cpu(), golden)
-    say("rational", down, res)
-    assert res["passed"], res
+    assert_parity(out, x, w1, w2, rational=True, tag=f"rational {down}")
 
 
 def test_repeat_calls_bitwise_and_poisoned_buffers():

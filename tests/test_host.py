@@ -90,7 +90,7 @@ def test_selection():
     p = problem_from_shapes([64, 128], [256, 128], [64, 256])
     plan = make_plan(p, Selection(down_impl="streamk"), 8)
     assert plan.workspace_bytes == plan.native.workspace_bytes > 0
-    assert plan.schedule()["down_sk_tiles"] == 1
+    assert plan.schedule()["down_sk_tiles"] >= 1
     with pytest.raises(NotApplicable):
         make_plan(p, Selection(down_impl="streamk"), 1)
     with pytest.raises(NotApplicable):   # H spans a single K iteration of a 64-deep tile
@@ -152,7 +152,6 @@ def test_split_up_schedule_covers_once_and_shares_every_tile(G):
     (the fixup, not the GEMM, applies its GELU), and its slots fit the workspace (brute force).
     Other up GEMMs keep one workgroup per tile."""
     lib = _lib.load()
-    sliced = _k_sliced_variants()
     split_seen = 0
     for (mp, kp, hp) in [(64, 5120, 1728), (64, 1024, 4096), (320, 1008, 448), (128, 256, 1024),
                          (4096, 1024, 4096), (64, 5120, 13824)]:
@@ -161,11 +160,11 @@ def test_split_up_schedule_covers_once_and_shares_every_tile(G):
             kI, tiles = n.up_k_iters, n.up_tiles
             assert kI == -(-kp // n.up_bk)
             if n.up_sk_tiles == 0:
-                assert tiles * 2 > G or kI < 16 or variant in sliced
+                assert tiles * 2 > G or kI < 16
                 assert n.up_grid == min(tiles, G)
                 continue
             split_seen += 1
-            assert n.up_sk_tiles == tiles and tiles * 2 <= G and kI >= 16 and variant not in sliced
+            assert n.up_sk_tiles == tiles and tiles * 2 <= G and kI >= 16
             Gs = n.up_grid
             assert tiles < Gs <= G
             q, r = divmod(tiles * kI, Gs)
@@ -333,40 +332,33 @@ def test_set_operands_validates_layout():
 
 
 def _k_sliced_variants():
-    """Variants with waves along K, found by behaviour: forced as the Stream-K down of a shape
-    every other tile splits (16 rows, 13824 deep, 5120 wide), they are refused as K-sliced."""
-    from ffn_optim_amd.host.dispatch import NotApplicable
+    """Variants with waves along K: the tenth field (WGK) of their row in ffn_variants.hpp."""
+    text = (REPO / "ffn_optim_amd" / "csrc" / "ffn_variants.hpp").read_text()
     out = set()
-    for v in range(_lib.load().ffn_mi355x_num_variants()):
-        try:
-            _lib.make_plan(64, 5120, 13824, 5120, _lib.BF16, "streamk", "erf", 256, 0, v, m=16)
-        except NotApplicable as exc:
-            assert "K-sliced" in str(exc), exc
-            out.add(v)
+    for m in re.finditer(r"^\s*X\(([^)]*)\)", text, re.M):
+        fields = [int(f) for f in m.group(1).split(",")]
+        if len(fields) >= 10 and fields[9] > 1:
+            out.add(fields[0])
     return out
 
 
-def test_k_sliced_variants_basic_only():
-    """The K-sliced tiles (two waves along K) are planned for the Basic down and the up GEMM,
-    report four or eight waves (one or two per SIMD), and have no Stream-K form."""
+def test_k_sliced_variants_plan_for_basic_and_streamk():
+    """The K-sliced tiles (two waves along K) report two, four or eight waves, are planned for
+    the up GEMM and the Basic down, and have a Stream-K form (the slices are summed before a
+    split piece writes its partial)."""
     from ffn_optim_amd import _lib
-    from ffn_optim_amd.host.dispatch import NotApplicable
     ids = _k_sliced_variants()
-    assert {10, 11, 13, 14} <= ids
+    assert {10, 11, 13, 14, 15, 16} == ids
     sliced = [v for v in _lib.variants() if v["variant"] in ids]
-    assert sliced, "no K-sliced variant compiled in"
     for v in sliced:
-        assert v["waves"] in (4, 8) and v["lds_bytes"] <= 160 * 1024
+        assert v["waves"] in (2, 4, 8) and v["lds_bytes"] <= 160 * 1024
         plan = _lib.make_plan(4096, 1024, 4096, 1024, _lib.BF16, "basic", "erf", 256,
                               v["variant"], v["variant"])
         assert (plan.up_variant, plan.down_variant) == (v["variant"], v["variant"])
         assert plan.workspace_bytes == 0
-        with pytest.raises(NotApplicable, match="K-sliced"):
-            _lib.make_plan(4096, 1024, 4096, 1024, _lib.BF16, "streamk", "erf", 256, 0, v["variant"])
-    # the planner's own Stream-K choice never lands on one
-    for mp, np_ in ((4096, 1024), (1024, 1024), (8192, 3072)):
-        plan = _lib.make_plan(mp, 1024, 4096, np_, _lib.BF16, "streamk", "erf", 256)
-        assert plan.down_variant not in {v["variant"] for v in sliced}
+        # decode down: 16 rows, 5120 wide, 13824 deep -- every tile count leaves a remainder
+        plan = _lib.make_plan(64, 5120, 13824, 5120, _lib.BF16, "streamk", "erf", 256, 8, v["variant"], m=16)
+        assert plan.down_variant == v["variant"] and plan.down_sk_tiles > 0 and plan.workspace_bytes > 0
 
 
 def test_run_rejects_a_plan_whose_launch_fields_were_changed():
