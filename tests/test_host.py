@@ -460,3 +460,25 @@ def test_compile_kernel_binds_a_plan_without_a_device():
         assert prov["down_impl"] == down and prov["entry_point"].startswith("ffn_mi355x_run")
         assert (prov["up_variant"], prov["down_variant"]) == (plan.up.variant, plan.down.variant)
         assert prov["version"].startswith("ffn_mi355x gfx950")
+
+
+# The tile each measured workload runs on, as the design notes' tile table states it:
+# (case id, down path) -> (up variant, down variant).
+TUNED_ASSIGNMENTS = {
+    ("c5_dit_bf16", "basic"): (12, 1), ("c5_dit_bf16", "streamk"): (12, 0),
+    ("c2_aligned_bf16", "basic"): (12, 13), ("c2_aligned_bf16", "streamk"): (12, 1),
+    ("c3_unaligned_fp16", "basic"): (13, 16), ("c3_unaligned_fp16", "streamk"): (13, 5),
+    ("c4_decode_bf16", "basic"): (14, 15), ("c4_decode_bf16", "streamk"): (14, 14),
+    ("c1_smoke_fp16", "basic"): (4, 15), ("c1_smoke_fp16", "streamk"): (4, 4),
+    ("c5_tp8_shard_bf16", "basic"): (0, 1), ("c5_tp8_shard_bf16", "streamk"): (13, 12),
+    ("c4_tp8_shard_bf16", "basic"): (15, 15), ("c4_tp8_shard_bf16", "streamk"): (15, 14),
+}
+
+
+@pytest.mark.parametrize("case_id,down", sorted(TUNED_ASSIGNMENTS))
+def test_tuned_table_assignments(case_id, down):
+    """Every workload plans to the variants the committed tuning table (and the design notes'
+    tile table) assign it, at 256 workgroups."""
+    from ffn_optim_amd.cases import get_case
+    plan = make_plan(case_problem(get_case(case_id)), Selection("basic", down), 256)
+    assert (plan.up.variant, plan.down.variant) == TUNED_ASSIGNMENTS[(case_id, down)]
