@@ -15,6 +15,8 @@ LIBRARY_PATH = Path(__file__).resolve().parent / "libffn_mi355x.so"
 FP16, BF16 = 0, 1
 DOWN_CODES = {"basic": 0, "streamk": 1, "full_load_a": 2, "full_load_b": 3}
 GELU_CODES = {"erf": 0, "rational": 1}
+# activation of the up epilogue (the GELU codes above, then SiLU and SwiGLU)
+ACTIVATION_CODES = {"gelu:erf": 0, "gelu:rational": 1, "silu": 2, "swiglu": 3}
 
 OK, EINVAL, ENOT_APPLICABLE, EUNAVAILABLE, EHIP, EDEVICE = 0, -1, -2, -3, -4, -5
 
@@ -23,7 +25,7 @@ class PlanStruct(ctypes.Structure):
     """Mirror of ``ffn_mi355x_plan``."""
 
     _fields_ = [(name, ctypes.c_int) for name in (
-        "m", "mp", "kp", "hp", "np", "dtype", "down_impl", "gelu", "block_num",
+        "m", "mp", "kp", "hp", "np", "dtype", "down_impl", "activation", "block_num",
         "up_variant", "down_variant", "up_bm", "up_bn", "up_bk",
         "down_bm", "down_bn", "down_bk", "up_tiles", "up_grid",
         "down_tiles", "down_grid", "down_k_iters", "down_dp_tiles",
@@ -46,6 +48,9 @@ SIGNATURES = {
     "ffn_mi355x_set_operands": (_i, [_P(PlanStruct), _i, _i, _i, _i, _i, _i]),
     "ffn_mi355x_run": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ffn_mi355x_run_noalloc": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ffn_mi355x_run_ex": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ffn_mi355x_up_ex": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ffn_mi355x_down_ex": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp]),
     "ffn_mi355x_up": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp]),
     "ffn_mi355x_down": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp]),
     "ffn_mi355x_num_variants": (_i, []),
@@ -109,14 +114,24 @@ def query(device: int) -> tuple[int, str]:
     return cus.value, arch.value.decode()
 
 
+def activation_code(activation="gelu", gelu="erf") -> int:
+    """Code of the up epilogue: a GELU form, SiLU or SwiGLU."""
+    key = f"gelu:{gelu}" if activation == "gelu" else activation
+    if key not in ACTIVATION_CODES:
+        raise ValueError(f"activation must be gelu, silu or swiglu and gelu erf or rational "
+                         f"(got {activation!r}, {gelu!r})")
+    return ACTIVATION_CODES[key]
+
+
 def make_plan(mp, kp, hp, np_, dtype, down_impl, gelu, block_num, up_variant=-1,
-              down_variant=-1, m=None) -> PlanStruct:
-    """Native plan; `m` is the logical row count (default: all mp rows hold data)."""
+              down_variant=-1, m=None, activation="gelu") -> PlanStruct:
+    """Native plan; `m` is the logical row count (default: all mp rows hold data); `gelu` is the
+    GELU form when activation is 'gelu'."""
     plan = PlanStruct()
     check(load().ffn_mi355x_make_plan(mp if m is None else m, mp, kp, hp, np_, dtype,
                                       DOWN_CODES[down_impl],
-                                      GELU_CODES[gelu], block_num, up_variant, down_variant,
-                                      ctypes.byref(plan)))
+                                      activation_code(activation, gelu), block_num, up_variant,
+                                      down_variant, ctypes.byref(plan)))
     return plan
 
 

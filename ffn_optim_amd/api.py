@@ -80,7 +80,8 @@ def _current_stream_handle(device):
 
 
 def prepare_ffn(x, weight1, weight2, *, up_impl="basic", down_impl="basic", block_num=None,
-                layout="linear", gelu="erf", up_variant=None, down_variant=None, _alias=False):
+                layout="linear", gelu="erf", up_variant=None, down_variant=None, activation="gelu",
+                bias1=None, bias2=None, _alias=False):
     """Validate, plan, check the device, pad/contiguise and bind the kernels; no FFN launch.
 
     Follows ops/api.py:48-89.  Padding and contiguisation are auxiliary device
@@ -88,11 +89,17 @@ def prepare_ffn(x, weight1, weight2, *, up_impl="basic", down_impl="basic", bloc
     tile variant (tuning); None lets the library choose.  The prepared storage is a
     snapshot of the inputs (later changes to x, weight1, weight2 do not reach run());
     ffn() alone, which runs at once, may use aligned inputs in place (_alias).
+
+    activation 'silu' or 'swiglu' (weight1 [2H, K]: gate rows, then up rows) and the
+    biases bias1 ([H] or [2H]) and bias2 ([N]), given together, select the other EagleFFN
+    paths, Y = act(X W1^T + b1) W2^T + b2 (spec/MindIE-SD EagleFFN算子实现分析.md:17-71); the
+    defaults are the reference's operator.  storage then ends with the two bias buffers.
     """
     from .host.dispatch import compile_kernel
     from . import _lib
 
-    p = validate_tensors(x, weight1, weight2, layout=layout, require_device=True)
+    p = validate_tensors(x, weight1, weight2, layout=layout, require_device=True,
+                         activation=activation, bias1=bias1, bias2=bias2)
     selection = Selection(up_impl, down_impl)
     selection.require_available()
     import torch
@@ -109,7 +116,8 @@ def prepare_ffn(x, weight1, weight2, *, up_impl="basic", down_impl="basic", bloc
         stream = torch.cuda.current_stream()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
-        storage, layout = prepare_storage(x, weight1, weight2, plan, alias_aligned=_alias)
+        storage, layout = prepare_storage(x, weight1, weight2, plan, alias_aligned=_alias,
+                                          bias1=bias1, bias2=bias2)
         end.record()
         _lib.set_operands(plan.native, *layout)
         end.synchronize()

@@ -39,7 +39,10 @@ typedef _Float16 f16x8 __attribute__((__vector_size__(16)));
 typedef __attribute__((address_space(3))) char lds_char;
 
 enum { DT_F16 = 0, DT_BF16 = 1 };
-enum { EPI_GELU_ERF = 0, EPI_GELU_RATIONAL = 1, EPI_STORE = 2 };
+// Epilogue of a GEMM role: the activation applied to the FP32 sum (plus bias) before the cast.
+// EPI_SWIGLU pairs 32-column blocks: block 2k holds gate columns, block 2k+1 the up columns of the
+// same 32 hidden columns (the weight rows are interleaved so), and SiLU(gate) * up is stored.
+enum { EPI_GELU_ERF = 0, EPI_GELU_RATIONAL = 1, EPI_STORE = 2, EPI_SILU = 3, EPI_SWIGLU = 4 };
 
 // Launch-time description of one GEMM.  All extents are in elements.
 struct GemmParams {
@@ -61,6 +64,9 @@ struct GemmParams {
     int fast_dma;         // 1: launch the kernel whose interior tiles refill through the SALU-addressed DMA path
     int rev_m;            // 1: tile rows are walked last-first
     int zero_row0;        // rows [zero_row0, M) of C lie past every tile holding data: written as zeros
+    int c_cols;           // columns of C (N, or N / 2 for SwiGLU, whose column pairs make one output)
+    const void* bias;     // per-column bias in the storage type, added in FP32 before the activation
+    int bias_n;           // bias values present; columns at or past bias_n add zero (NULL bias: none)
 };
 
 // SYNCQ_: MFMA slot of a stage's last k-step after which the stage wait + barrier is placed
@@ -237,11 +243,46 @@ __device__ __forceinline__ float gelu_rational(float z) {
     return (z * 0.5f) * (p * __builtin_amdgcn_rcpf(q) + 1.0f);
 }
 
+// SiLU(z) = z / (1 + e^-z) (analysis doc of the EagleFFN baseline, :52-56): one v_exp_f32 and one
+// v_rcp_f32.  For z -> -inf, e^-z overflows to inf and the result is -0; for z -> +inf it is z.
+__device__ __forceinline__ float silu(float z) {
+    constexpr float L2E = 1.4426950408889634f;
+    return z * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-z * L2E));
+}
+
 template <int EPI>
 __device__ __forceinline__ float activate(float z) {
     if constexpr (EPI == EPI_GELU_ERF) return gelu_erf(z);
     else if constexpr (EPI == EPI_GELU_RATIONAL) return gelu_rational(z);
+    else if constexpr (EPI == EPI_SILU) return silu(z);
     else return z;
+}
+
+// Storage value -> FP32 (exact).
+template <int DT>
+__device__ __forceinline__ float to_f32(uint32_t bits16) {
+    if constexpr (DT == DT_BF16) return __builtin_bit_cast(float, bits16 << 16);
+    else return (float)__builtin_bit_cast(_Float16, (unsigned short)bits16);
+}
+
+// Bias of columns n..n+3 (n a multiple of 4) in FP32; zero past bias_n.  Only called by the
+// epilogue bodies instantiated for a bias (p.bias set): the kernels test p.bias once per tile and
+// run a body without bias terms otherwise, so the bias-free epilogue is branch-free.
+template <int DT>
+__device__ __forceinline__ f32x4 bias4(const GemmParams& p, int n) {
+    f32x4 b = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (n + 4 <= p.bias_n) {
+        const u32x2 w = *(const u32x2*)((const char*)p.bias + (size_t)n * 2);
+        b = f32x4{to_f32<DT>(w.x & 0xffffu), to_f32<DT>(w.x >> 16), to_f32<DT>(w.y & 0xffffu),
+                  to_f32<DT>(w.y >> 16)};
+    } else if (n < p.bias_n) {
+        // the last values: element loads, none past the bias
+        const unsigned short* e = (const unsigned short*)p.bias + n;
+        b.x = to_f32<DT>(e[0]);
+        if (n + 1 < p.bias_n) b.y = to_f32<DT>(e[1]);
+        if (n + 2 < p.bias_n) b.z = to_f32<DT>(e[2]);
+    }
+    return b;
 }
 
 // tile index -> (tile row, tile column); tiles walk `group_m` tile-rows column by column so
@@ -709,8 +750,10 @@ struct Engine {
 
     // Activate and cast the blocks of chunk c in registers: group (j, i, q) packs into words
     // 2q, 2q+1 of acc[j][i], whose sources are already consumed.
-    template <int EPI>
-    __device__ __forceinline__ void activate_chunk(int c, f32x16 (&acc)[FN][FM]) const {
+    template <int EPI, bool BIAS>
+    __device__ __forceinline__ void activate_chunk(const GemmParams& p, const Unit& u, int c,
+                                                   f32x16 (&acc)[FN][FM]) const {
+        const int bcol = u.tn * C::BN + wn * C::WTN + 4 * (lane >> 5);
 #pragma unroll
         for (int ib = 0; ib < BPC; ++ib) {
             const int i = c * BPC + ib;
@@ -718,10 +761,7 @@ struct Engine {
             for (int j = 0; j < FN; ++j) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    const u32x2 v = pack4<DT>(activate<EPI>(acc[j][i][4 * q]),
-                                              activate<EPI>(acc[j][i][4 * q + 1]),
-                                              activate<EPI>(acc[j][i][4 * q + 2]),
-                                              activate<EPI>(acc[j][i][4 * q + 3]));
+                    const u32x2 v = out4<EPI, BIAS>(p, acc[j][i], q, bcol + 32 * j + 8 * q);
                     acc[j][i][2 * q] = u2f(v.x);
                     acc[j][i][2 * q + 1] = u2f(v.y);
                 }
@@ -733,6 +773,12 @@ struct Engine {
     template <int EPI>
     __device__ __forceinline__ void store_tile_lds(const GemmParams& p, const Unit& u, bool next,
                                                    f32x16 (&acc)[FN][FM]) {
+        if (p.bias) store_tile_lds_as<EPI, true>(p, u, next, acc);
+        else store_tile_lds_as<EPI, false>(p, u, next, acc);
+    }
+    template <int EPI, bool BIAS>
+    __device__ __forceinline__ void store_tile_lds_as(const GemmParams& p, const Unit& u, bool next,
+                                                      f32x16 (&acc)[FN][FM]) {
         lds_char* eb = smem + C::EPI_OFF;
         // DMA still in flight may target any stage but the next unit's prologue (issued last):
         // drain it; the barrier before the first staging write makes sure every wave has
@@ -744,7 +790,7 @@ struct Engine {
         int ln = lane, td = tid;
         asm volatile("" : "+v"(ln));
         asm volatile("" : "+v"(td));
-        activate_chunk<EPI>(0, acc);
+        activate_chunk<EPI, BIAS>(p, u, 0, acc);
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
             barrier();
@@ -781,13 +827,13 @@ struct Engine {
                     v[k] = *(const __attribute__((address_space(3))) u32x4*)(eb + out_off(s, ch));
                 }
                 __builtin_amdgcn_sched_barrier(0);
-                if (k0 == 0 && c + 1 < NCH) activate_chunk<EPI>(c + 1, acc);
+                if (k0 == 0 && c + 1 < NCH) activate_chunk<EPI, BIAS>(p, u, c + 1, acc);
 #pragma unroll
                 for (int k = 0; k < PB; ++k) {
                     const int idx = (k0 + k) * NT + td;
                     const int s = idx / TPR, ch = idx - s * TPR;
                     const int gm = row0 + (s / ERW) * C::WTM + c * ERW + (s % ERW), gn = col0 + ch * 8;
-                    if (gm < p.M && gn < p.N)
+                    if (gm < p.M && gn < p.c_cols)
                         *(u32x4*)((char*)p.c + ((size_t)gm * (size_t)p.ldc + (size_t)gn) * 2) = v[k];
                 }
                 __builtin_amdgcn_sched_barrier(0);
@@ -803,33 +849,80 @@ struct Engine {
     // lane (32 rows x 32 contiguous bytes per instruction), with no LDS round trip and no
     // barrier, so the next unit's main loop starts as soon as the stores are issued.  Row
     // blocks [I0, I1) of the wave tile are stored.
+    // Bias (if any) added to acc's columns: group q of block j holds columns
+    // col0 + 32j + 8q + 4h + 0..3 of the tile, h = lane >> 5.
+    template <int EPI, bool BIAS>
+    __device__ __forceinline__ u32x2 out4(const GemmParams& p, const f32x16& a, int q, int col) const {
+        if constexpr (BIAS) {
+            const f32x4 b = bias4<DT>(p, col);
+            return pack4<DT>(activate<EPI>(a[4 * q] + b.x), activate<EPI>(a[4 * q + 1] + b.y),
+                             activate<EPI>(a[4 * q + 2] + b.z), activate<EPI>(a[4 * q + 3] + b.w));
+        } else {
+            return pack4<DT>(activate<EPI>(a[4 * q]), activate<EPI>(a[4 * q + 1]), activate<EPI>(a[4 * q + 2]),
+                             activate<EPI>(a[4 * q + 3]));
+        }
+    }
+    // SwiGLU: SiLU(gate + its bias) * (up + its bias) of the matching groups of a block pair.
+    template <bool BIAS>
+    __device__ __forceinline__ u32x2 swiglu4(const GemmParams& p, const f32x16& g, const f32x16& up, int q,
+                                             int gcol, int ucol) const {
+        f32x4 bg = {0.0f, 0.0f, 0.0f, 0.0f}, bu = bg;
+        if constexpr (BIAS) bg = bias4<DT>(p, gcol), bu = bias4<DT>(p, ucol);
+        return pack4<DT>(silu(g[4 * q] + bg.x) * (up[4 * q] + bu.x), silu(g[4 * q + 1] + bg.y) * (up[4 * q + 1] + bu.y),
+                         silu(g[4 * q + 2] + bg.z) * (up[4 * q + 2] + bu.z),
+                         silu(g[4 * q + 3] + bg.w) * (up[4 * q + 3] + bu.w));
+    }
+    // Lanes l and l + 32 hold the two 16-byte halves of 16 consecutive output columns after one
+    // v_permlane32_swap per word; n0 is the first output column of the lane's 32-column block.
+    __device__ __forceinline__ void store_block(const GemmParams& p, char* row, int m, int n0, const u32x2 (&g)[4]) const {
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp) {
+            const auto s0 = __builtin_amdgcn_permlane32_swap(g[2 * pp].x, g[2 * pp + 1].x, false, false);
+            const auto s1 = __builtin_amdgcn_permlane32_swap(g[2 * pp].y, g[2 * pp + 1].y, false, false);
+            const u32x4 v = {(uint32_t)s0[0], (uint32_t)s1[0], (uint32_t)s0[1], (uint32_t)s1[1]};
+            const int n = n0 + 16 * pp;
+            if (m < p.M && n < p.c_cols) *(u32x4*)(row + (size_t)n * 2) = v;
+        }
+    }
     template <int EPI, int I0 = 0, int I1 = FM>
     __device__ __forceinline__ void store_tile_regs(const GemmParams& p, const Unit& u,
                                                     f32x16 (&acc)[FN][FM]) const {
+        if (p.bias) store_tile_regs_as<EPI, I0, I1, true>(p, u, acc);
+        else store_tile_regs_as<EPI, I0, I1, false>(p, u, acc);
+    }
+    template <int EPI, int I0, int I1, bool BIAS>
+    __device__ __forceinline__ void store_tile_regs_as(const GemmParams& p, const Unit& u,
+                                                       f32x16 (&acc)[FN][FM]) const {
         int ln = lane;
         asm volatile("" : "+v"(ln));
         const int m0 = u.tm * C::BM + wm * C::WTM + (ln & 31);
-        const int n0 = u.tn * C::BN + wn * C::WTN + 8 * (ln >> 5);
+        const int col0 = u.tn * C::BN + wn * C::WTN;  // first column of the wave tile
+        const int bcol = col0 + 4 * (ln >> 5);         // bias column of group q = 0, block 0
 #pragma unroll
         for (int i = I0; i < I1; ++i) {
             const int m = m0 + 32 * i;
             char* row = (char*)p.c + (size_t)m * (size_t)p.ldc * 2;
+            if constexpr (EPI == EPI_SWIGLU) {
+                static_assert(FN % 2 == 0, "SwiGLU pairs the 32-column blocks of a wave tile");
 #pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                u32x2 g[4];
+                for (int k = 0; k < FN / 2; ++k) {
+                    u32x2 g[4];
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    g[q] = pack4<DT>(activate<EPI>(acc[j][i][4 * q]), activate<EPI>(acc[j][i][4 * q + 1]),
-                                     activate<EPI>(acc[j][i][4 * q + 2]), activate<EPI>(acc[j][i][4 * q + 3]));
-#pragma unroll
-                for (int pp = 0; pp < 2; ++pp) {
-                    const auto s0 = __builtin_amdgcn_permlane32_swap(g[2 * pp].x, g[2 * pp + 1].x, false, false);
-                    const auto s1 = __builtin_amdgcn_permlane32_swap(g[2 * pp].y, g[2 * pp + 1].y, false, false);
-                    const u32x4 v = {(uint32_t)s0[0], (uint32_t)s1[0], (uint32_t)s0[1], (uint32_t)s1[1]};
-                    const int n = n0 + 32 * j + 16 * pp;
-                    if (m < p.M && n < p.N) *(u32x4*)(row + (size_t)n * 2) = v;
+                    for (int q = 0; q < 4; ++q)
+                        g[q] = swiglu4<BIAS>(p, acc[2 * k][i], acc[2 * k + 1][i], q, bcol + 64 * k + 8 * q,
+                                             bcol + 64 * k + 32 + 8 * q);
+                    store_block(p, row, m, col0 / 2 + 32 * k + 8 * (ln >> 5), g);
+                    __builtin_amdgcn_sched_barrier(0);
                 }
-                __builtin_amdgcn_sched_barrier(0);
+            } else {
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    u32x2 g[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) g[q] = out4<EPI, BIAS>(p, acc[j][i], q, bcol + 32 * j + 8 * q);
+                    store_block(p, row, m, col0 + 32 * j + 8 * (ln >> 5), g);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             }
         }
     }
@@ -982,7 +1075,7 @@ __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
     // Output rows past the last tile row that holds data (zero padding of a small-M problem) are
     // not computed: every workgroup writes its share of them as zeros, ahead of its first unit.
     if (p.zero_row0 < p.M) {
-        const int cpr = p.N / 8;  // 16-byte chunks per row
+        const int cpr = p.c_cols / 8;  // 16-byte chunks per row
         const long long total = (long long)(p.M - p.zero_row0) * cpr;
         for (long long i = (long long)g * C::NT + threadIdx.x; i < total; i += (long long)G * C::NT) {
             const long long r = p.zero_row0 + i / cpr, c = i % cpr;
@@ -1020,6 +1113,7 @@ __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
 // two 16-byte row segments.
 template <int DT, class C, int EPI>
 __global__ void __launch_bounds__(C::NT) ffn_sk_reduce_kernel(GemmParams p, int blocks) {
+    static_assert(EPI != EPI_SWIGLU, "a SwiGLU up GEMM is never split: its block pairs leave together");
     constexpr int TE = C::BM * C::BN;
     const int s = blockIdx.x / blocks, ji = blockIdx.x - s * blocks;
     const int kI = p.k_iters;
@@ -1044,6 +1138,11 @@ __global__ void __launch_bounds__(C::NT) ffn_sk_reduce_kernel(GemmParams p, int 
 #pragma unroll
         for (int q = 0; q < 4; ++q) tot[q] += *(const f32x4*)(slot + ((size_t)(ji * 4 + q) * NTL + tid) * 4);
     }
+    const int bcol = tn * C::BN + wn * C::WTN + 32 * j + 4 * (lane >> 5);
+    if (p.bias) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) tot[q] += bias4<DT>(p, bcol + 8 * q);
+    }
     u32x2 g[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q)
@@ -1057,7 +1156,7 @@ __global__ void __launch_bounds__(C::NT) ffn_sk_reduce_kernel(GemmParams p, int 
         const auto s1 = __builtin_amdgcn_permlane32_swap(g[2 * pp].y, g[2 * pp + 1].y, false, false);
         const u32x4 v = {(uint32_t)s0[0], (uint32_t)s1[0], (uint32_t)s0[1], (uint32_t)s1[1]};
         const int n = n0 + 16 * pp;
-        if (m < p.M && n < p.N) *(u32x4*)((char*)p.c + ((size_t)m * (size_t)p.ldc + (size_t)n) * 2) = v;
+        if (m < p.M && n < p.c_cols) *(u32x4*)((char*)p.c + ((size_t)m * (size_t)p.ldc + (size_t)n) * 2) = v;
     }
 }
 

@@ -86,6 +86,16 @@ hipError_t launch_role(int role, const ffn::GemmParams* p, int grid, hipStream_t
         case FFN_ROLE_UP_SPLIT_RATIONAL:
             e = launch_split<CFG, EPI_GELU_RATIONAL>(p, g, b, stream);
             break;
+        case FFN_ROLE_UP_SILU:
+            launch_gemm<CFG, EPI_SILU, false>(p, g, b, stream);
+            break;
+        case FFN_ROLE_UP_SWIGLU:
+            if constexpr (CFG::WTN % 64 == 0) launch_gemm<CFG, EPI_SWIGLU, false>(p, g, b, stream);
+            else return hipErrorInvalidValue;
+            break;
+        case FFN_ROLE_UP_SPLIT_SILU:
+            e = launch_split<CFG, EPI_SILU>(p, g, b, stream);
+            break;
         default:
             return hipErrorInvalidValue;
     }

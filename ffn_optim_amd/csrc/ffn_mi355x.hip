@@ -237,13 +237,20 @@ bool split_up(const Variant& v, long long m_valid, long long N, long long K, int
 
 // Up-GEMM tile when none is forced: every variant is priced as the plan it would get, split
 // along K (Stream-K cost, fixup included) or one workgroup per tile.
-int pick_up(long long M, long long m_valid, long long N, long long K, int G) {
-    int best = 0;
+// A SwiGLU up GEMM (N = 2 x the hidden width, gate and up rows interleaved in 32-row blocks)
+// needs wave tiles of whole block pairs and is never split (a split tile's blocks would be
+// finished one by one by the fixup, apart from their partners).
+bool swiglu_tile(const Variant& v) { return (v.bn / v.wgn) % 64 == 0; }
+
+int pick_up(long long M, long long m_valid, long long N, long long K, int G, bool swiglu) {
+    int best = -1;
     double best_cost = 1e300;
     for (int i = 0; i < kNumVariants; ++i) {
+        if (swiglu && !swiglu_tile(kVariants[i])) continue;
         SkShape s;
-        const double c = split_up(kVariants[i], m_valid, N, K, G, s) ? cost_streamk(kVariants[i], s, m_valid, N, K)
-                                                                : cost_basic(kVariants[i], M, m_valid, N, K, G);
+        const double c = !swiglu && split_up(kVariants[i], m_valid, N, K, G, s)
+                             ? cost_streamk(kVariants[i], s, m_valid, N, K)
+                             : cost_basic(kVariants[i], M, m_valid, N, K, G);
         if (c < best_cost * 0.999) best_cost = c, best = i;
     }
     return best;
@@ -320,7 +327,7 @@ unsigned long long plan_stamp(const ffn_mi355x_plan* p) {
             h *= 0x100000001b3ull;
         }
     };
-    const int ints[] = {p->m, p->mp, p->kp, p->hp, p->np, p->dtype, p->down_impl, p->gelu, p->block_num,
+    const int ints[] = {p->m, p->mp, p->kp, p->hp, p->np, p->dtype, p->down_impl, p->activation, p->block_num,
                         p->up_variant, p->down_variant, p->up_bm, p->up_bn, p->up_bk, p->down_bm, p->down_bn,
                         p->down_bk, p->up_tiles, p->up_grid, p->down_tiles, p->down_grid, p->down_k_iters,
                         p->down_dp_tiles, p->down_sk_tiles, p->down_slots_per_wg, p->k, p->h, p->n, p->ldx,
@@ -339,7 +346,7 @@ bool valid_plan(const ffn_mi355x_plan* p) {
            p->up_variant < kNumVariants && p->down_variant >= 0 && p->down_variant < kNumVariants &&
            (p->dtype == 0 || p->dtype == 1) &&
            (p->down_impl == FFN_MI355X_DOWN_BASIC || p->down_impl == FFN_MI355X_DOWN_STREAMK) &&
-           (p->gelu == 0 || p->gelu == 1) && p->block_num >= 1;
+           p->activation >= FFN_MI355X_GELU_ERF && p->activation <= FFN_MI355X_SWIGLU && p->block_num >= 1;
 }
 
 int launch(const Variant& v, int dtype, int role, const ffn::GemmParams& gp, int grid,
@@ -370,15 +377,16 @@ int ffn_mi355x_query(int device, int* cu_count, char* arch, int arch_len) {
     return ok();
 }
 
-int ffn_mi355x_make_plan(int m, int mp, int kp, int hp, int np, int dtype, int down_impl, int gelu,
+int ffn_mi355x_make_plan(int m, int mp, int kp, int hp, int np, int dtype, int down_impl, int activation,
                          int block_num, int up_variant, int down_variant, ffn_mi355x_plan* plan) {
     if (!plan) return fail(FFN_MI355X_EINVAL, "plan must not be NULL");
     if (m <= 0 || m > mp)
         return fail(FFN_MI355X_EINVAL, "logical rows m must be in [1, mp] (got m=%d mp=%d)", m, mp);
     if (dtype != FFN_MI355X_FP16 && dtype != FFN_MI355X_BF16)
         return fail(FFN_MI355X_EINVAL, "dtype must be float16 or bfloat16");
-    if (gelu != FFN_MI355X_GELU_ERF && gelu != FFN_MI355X_GELU_RATIONAL)
-        return fail(FFN_MI355X_EINVAL, "gelu must be erf or rational");
+    if (activation < FFN_MI355X_GELU_ERF || activation > FFN_MI355X_SWIGLU)
+        return fail(FFN_MI355X_EINVAL, "activation must be erf GELU, rational GELU, SiLU or SwiGLU");
+    const bool swiglu = activation == FFN_MI355X_SWIGLU;
     if (down_impl == FFN_MI355X_DOWN_FULL_LOAD_A || down_impl == FFN_MI355X_DOWN_FULL_LOAD_B)
         return fail(FFN_MI355X_EUNAVAILABLE, "%s: no gfx950 kernel is provided for this down variant; no fallback",
                     down_impl == FFN_MI355X_DOWN_FULL_LOAD_A ? "full_load_a" : "full_load_b");
@@ -399,20 +407,24 @@ int ffn_mi355x_make_plan(int m, int mp, int kp, int hp, int np, int dtype, int d
     memset(plan, 0, sizeof *plan);
     plan->m = m;
     plan->mp = mp, plan->kp = kp, plan->hp = hp, plan->np = np;
-    plan->dtype = dtype, plan->down_impl = down_impl, plan->gelu = gelu, plan->block_num = block_num;
+    plan->dtype = dtype, plan->down_impl = down_impl, plan->activation = activation, plan->block_num = block_num;
     const int G = block_num;
 
-    // up: [mp x hp], depth kp
-    const int uv = up_variant >= 0 ? up_variant : pick_up(mp, m, hp, kp, G);
+    // up: [mp x hp], depth kp (SwiGLU: [mp x 2hp], gate and up column blocks interleaved)
+    const long long un = swiglu ? 2LL * hp : hp;
+    if (swiglu && up_variant >= 0 && !swiglu_tile(kVariants[up_variant]))
+        return fail(FFN_MI355X_EINVAL, "SwiGLU needs an up tile whose wave tiles are multiples of 64 columns "
+                    "(variant %d is not)", up_variant);
+    const int uv = up_variant >= 0 ? up_variant : pick_up(mp, m, un, kp, G, swiglu);
     const Variant& U = kVariants[uv];
     plan->up_variant = uv;
     plan->up_bm = U.bm, plan->up_bn = U.bn, plan->up_bk = U.bk;
-    plan->up_tiles = (int)(cdiv(m, U.bm) * cdiv(hp, U.bn));
+    plan->up_tiles = (int)(cdiv(m, U.bm) * cdiv(un, U.bn));
     plan->up_grid = plan->up_tiles < G ? plan->up_tiles : G;
     plan->up_k_iters = (int)cdiv(kp, U.bk);
     size_t up_ws = 0;
     SkShape su;
-    if (split_up(U, m, hp, kp, G, su)) {
+    if (!swiglu && split_up(U, m, hp, kp, G, su)) {
         plan->up_sk_tiles = (int)su.sk;
         plan->up_slots_per_wg = (int)su.slots;
         plan->up_grid = (int)su.grid;
@@ -502,18 +514,24 @@ namespace {
 
 // Up GEMM of a plan.  ws_scratch: ws is this library's scratch array (its size is known, and it
 // is not a HIP allocation of its own to look up).
-int run_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, void* hidden, void* ws,
+// Rows of W1 a plan reads: the logical H, or for SwiGLU the 2 hp interleaved gate and up rows.
+long long w1_rows(const ffn_mi355x_plan* p) { return p->activation == FFN_MI355X_SWIGLU ? 2LL * p->hp : p->h; }
+
+int run_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, const void* b1, void* hidden, void* ws,
            bool ws_scratch, void* hip_stream) {
     if (!valid_plan(plan)) return fail(FFN_MI355X_EINVAL, "invalid plan");
     if (!x || !w1 || !hidden) return fail(FFN_MI355X_EINVAL, "NULL device buffer");
-    if (!aligned16(x) || !aligned16(w1) || !aligned16(hidden) || (ws && !aligned16(ws)))
+    if (!aligned16(x) || !aligned16(w1) || !aligned16(hidden) || (ws && !aligned16(ws)) || (b1 && !aligned16(b1)))
         return fail(FFN_MI355X_EINVAL, "device buffers must be 16-byte aligned");
     const bool split = plan->up_sk_tiles > 0;
+    const bool swiglu = plan->activation == FFN_MI355X_SWIGLU;
     if (split && !ws)
         return fail(FFN_MI355X_EINVAL, "the split up GEMM needs a workspace of %zu bytes", plan->workspace_bytes);
+    const long long rows = w1_rows(plan);
     int rc;
     if ((rc = check_span("x", x, span_bytes(plan->m, plan->ldx, plan->k))) != FFN_MI355X_OK ||
-        (rc = check_span("w1", w1, span_bytes(plan->h, plan->ldw1, plan->k))) != FFN_MI355X_OK ||
+        (rc = check_span("w1", w1, span_bytes(rows, plan->ldw1, plan->k))) != FFN_MI355X_OK ||
+        (b1 && (rc = check_span("bias1", b1, (size_t)rows * 2u)) != FFN_MI355X_OK) ||
         (rc = check_span("hidden", hidden, span_bytes(plan->mp, plan->hp, plan->hp))) != FFN_MI355X_OK ||
         (split && !ws_scratch && (rc = check_span("ws", ws, plan->workspace_bytes)) != FFN_MI355X_OK))
         return rc;
@@ -521,19 +539,21 @@ int run_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, void* hid
     ffn::GemmParams gp;
     memset(&gp, 0, sizeof gp);
     gp.a = x, gp.b = w1, gp.c = hidden;
-    // all hp hidden columns are written: those past h from zero rows of W1, GELU(0) = 0
-    gp.M = plan->mp, gp.N = plan->hp, gp.K = plan->k;
-    gp.m_valid = plan->m, gp.n_valid = plan->h;
+    // all hp hidden columns are written: those past h from zero rows of W1 (act(0) = 0 for every
+    // activation, and a bias reads as zero past h)
+    gp.M = plan->mp, gp.N = (int)(swiglu ? 2LL * plan->hp : plan->hp), gp.K = plan->k;
+    gp.c_cols = plan->hp;
+    gp.m_valid = plan->m, gp.n_valid = (int)rows;
     gp.lda = plan->ldx, gp.ldb = plan->ldw1, gp.ldc = plan->hp;
-    gp.tiles_m = (int)cdiv(plan->m, U.bm), gp.tiles_n = (int)cdiv(plan->hp, U.bn);
+    gp.tiles_m = (int)cdiv(plan->m, U.bm), gp.tiles_n = (int)cdiv(gp.N, U.bn);
     gp.zero_row0 = (int)std::min<long long>(plan->mp, (long long)gp.tiles_m * U.bm);
     gp.k_iters = plan->up_k_iters;
     gp.dp_tiles = gp.tiles_m * gp.tiles_n;
     gp.group_m = group_m_for(gp.tiles_m);
     gp.fast_dma = fast_dma_for(gp.K);
-    const bool erf = plan->gelu == FFN_MI355X_GELU_ERF;
+    gp.bias = b1, gp.bias_n = b1 ? (int)rows : 0;
     if (split) {
-        // every tile split (no whole tiles): FP32 partials, then the fixup with the GELU
+        // every tile split (no whole tiles): FP32 partials, then the fixup with the activation
         const long long total = (long long)plan->up_sk_tiles * plan->up_k_iters;
         gp.dp_tiles = 0;
         gp.sk_tiles = plan->up_sk_tiles;
@@ -541,23 +561,29 @@ int run_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, void* hid
         gp.sk_r = (int)(total % plan->up_grid);
         gp.slots_per_wg = plan->up_slots_per_wg;
         gp.ws = (float*)ws;
-        return launch(U, plan->dtype, erf ? FFN_ROLE_UP_SPLIT_ERF : FFN_ROLE_UP_SPLIT_RATIONAL, gp,
-                      plan->up_grid, hip_stream);
+        const int role = plan->activation == FFN_MI355X_GELU_ERF        ? FFN_ROLE_UP_SPLIT_ERF
+                         : plan->activation == FFN_MI355X_GELU_RATIONAL ? FFN_ROLE_UP_SPLIT_RATIONAL
+                                                                        : FFN_ROLE_UP_SPLIT_SILU;
+        return launch(U, plan->dtype, role, gp, plan->up_grid, hip_stream);
     }
-    return launch(U, plan->dtype, erf ? FFN_ROLE_UP_ERF : FFN_ROLE_UP_RATIONAL, gp, plan->up_grid,
-                  hip_stream);
+    const int role = plan->activation == FFN_MI355X_GELU_ERF        ? FFN_ROLE_UP_ERF
+                     : plan->activation == FFN_MI355X_GELU_RATIONAL ? FFN_ROLE_UP_RATIONAL
+                     : plan->activation == FFN_MI355X_SILU          ? FFN_ROLE_UP_SILU
+                                                                    : FFN_ROLE_UP_SWIGLU;
+    return launch(U, plan->dtype, role, gp, plan->up_grid, hip_stream);
 }
 
 // Down GEMM of a plan (ws_scratch as for run_up).
-int run_down(const ffn_mi355x_plan* plan, const void* hidden, const void* w2, void* out, void* ws,
+int run_down(const ffn_mi355x_plan* plan, const void* hidden, const void* w2, const void* b2, void* out, void* ws,
              bool ws_scratch, void* hip_stream) {
     if (!valid_plan(plan)) return fail(FFN_MI355X_EINVAL, "invalid plan");
     if (!hidden || !w2 || !out) return fail(FFN_MI355X_EINVAL, "NULL device buffer");
-    if (!aligned16(hidden) || !aligned16(w2) || !aligned16(out) || (ws && !aligned16(ws)))
+    if (!aligned16(hidden) || !aligned16(w2) || !aligned16(out) || (ws && !aligned16(ws)) || (b2 && !aligned16(b2)))
         return fail(FFN_MI355X_EINVAL, "device buffers must be 16-byte aligned");
     int rc;
     if ((rc = check_span("hidden", hidden, span_bytes(plan->m, plan->hp, down_depth(plan)))) != FFN_MI355X_OK ||
         (rc = check_span("w2", w2, span_bytes(plan->n, plan->ldw2, down_depth(plan)))) != FFN_MI355X_OK ||
+        (b2 && (rc = check_span("bias2", b2, (size_t)plan->n * 2u)) != FFN_MI355X_OK) ||
         (rc = check_span("out", out, span_bytes(plan->mp, plan->np, plan->np))) != FFN_MI355X_OK ||
         (plan->down_impl == FFN_MI355X_DOWN_STREAMK && ws && !ws_scratch &&
          (rc = check_span("ws", ws, plan->workspace_bytes)) != FFN_MI355X_OK))
@@ -567,6 +593,8 @@ int run_down(const ffn_mi355x_plan* plan, const void* hidden, const void* w2, vo
     memset(&gp, 0, sizeof gp);
     gp.a = hidden, gp.b = w2, gp.c = out;
     gp.M = plan->mp, gp.N = plan->np, gp.K = down_depth(plan);
+    gp.c_cols = plan->np;
+    gp.bias = b2, gp.bias_n = b2 ? plan->n : 0;
     gp.m_valid = plan->m, gp.n_valid = plan->n;
     gp.lda = plan->hp, gp.ldb = plan->ldw2, gp.ldc = plan->np;
     gp.tiles_m = (int)cdiv(plan->m, D.bm), gp.tiles_n = (int)cdiv(plan->np, D.bn);
@@ -642,19 +670,38 @@ extern "C" {
 
 int ffn_mi355x_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, void* hidden,
                   void* ws, void* hip_stream) {
-    return run_up(plan, x, w1, hidden, ws, false, hip_stream);
+    return run_up(plan, x, w1, nullptr, hidden, ws, false, hip_stream);
 }
 
 int ffn_mi355x_down(const ffn_mi355x_plan* plan, const void* hidden, const void* w2, void* out,
                     void* ws, void* hip_stream) {
-    return run_down(plan, hidden, w2, out, ws, false, hip_stream);
+    return run_down(plan, hidden, w2, nullptr, out, ws, false, hip_stream);
 }
 
 int ffn_mi355x_run(const ffn_mi355x_plan* plan, const void* x, const void* w1, const void* w2,
                    void* hidden, void* out, void* ws, void* hip_stream) {
-    int rc = run_up(plan, x, w1, hidden, ws, false, hip_stream);
+    int rc = run_up(plan, x, w1, nullptr, hidden, ws, false, hip_stream);
     if (rc != FFN_MI355X_OK) return rc;
-    return run_down(plan, hidden, w2, out, ws, false, hip_stream);
+    return run_down(plan, hidden, w2, nullptr, out, ws, false, hip_stream);
+}
+
+int ffn_mi355x_up_ex(const ffn_mi355x_plan* plan, const void* x, const void* w1, const void* b1, void* hidden,
+                     void* ws, void* hip_stream) {
+    return run_up(plan, x, w1, b1, hidden, ws, false, hip_stream);
+}
+
+int ffn_mi355x_down_ex(const ffn_mi355x_plan* plan, const void* hidden, const void* w2, const void* b2,
+                       void* out, void* ws, void* hip_stream) {
+    return run_down(plan, hidden, w2, b2, out, ws, false, hip_stream);
+}
+
+int ffn_mi355x_run_ex(const ffn_mi355x_plan* plan, const void* x, const void* w1, const void* b1,
+                      const void* w2, const void* b2, void* hidden, void* out, void* ws, void* hip_stream) {
+    if ((b1 == nullptr) != (b2 == nullptr))
+        return fail(FFN_MI355X_EINVAL, "bias1 and bias2 are given together or not at all");
+    int rc = run_up(plan, x, w1, b1, hidden, ws, false, hip_stream);
+    if (rc != FFN_MI355X_OK) return rc;
+    return run_down(plan, hidden, w2, b2, out, ws, false, hip_stream);
 }
 
 int ffn_mi355x_run_noalloc(const ffn_mi355x_plan* plan, const void* x, const void* w1, const void* w2,
@@ -670,9 +717,9 @@ int ffn_mi355x_run_noalloc(const ffn_mi355x_plan* plan, const void* x, const voi
         const int rc = scratch_address(hip_stream, &ws);
         if (rc != FFN_MI355X_OK) return rc;
     }
-    int rc = run_up(plan, x, w1, hidden, ws, true, hip_stream);
+    int rc = run_up(plan, x, w1, nullptr, hidden, ws, true, hip_stream);
     if (rc != FFN_MI355X_OK) return rc;
-    return run_down(plan, hidden, w2, out, ws, true, hip_stream);
+    return run_down(plan, hidden, w2, nullptr, out, ws, true, hip_stream);
 }
 
 int ffn_mi355x_num_variants(void) { return kNumVariants; }

@@ -50,5 +50,8 @@ enum {
     FFN_ROLE_DOWN_BASIC = 2,
     FFN_ROLE_DOWN_STREAMK = 3,
     FFN_ROLE_UP_SPLIT_ERF = 4,
-    FFN_ROLE_UP_SPLIT_RATIONAL = 5
+    FFN_ROLE_UP_SPLIT_RATIONAL = 5,
+    FFN_ROLE_UP_SILU = 6,
+    FFN_ROLE_UP_SWIGLU = 7,       // tiles with wave tiles of whole 64-column block pairs only
+    FFN_ROLE_UP_SPLIT_SILU = 8
 };

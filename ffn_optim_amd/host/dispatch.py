@@ -85,10 +85,16 @@ def compile_kernel(plan):
     lib = _lib.load()
     native = plan.native
     plan_ref = ctypes.byref(native)
-    run = lib.ffn_mi355x_run
+    run, run_ex = lib.ffn_mi355x_run, lib.ffn_mi355x_run_ex
 
-    def artifact(x, w1, w2, hidden, out, ws, stream):
-        rc = run(plan_ref, x, w1, w2, hidden, out, ws, stream)
+    def artifact(x, w1, w2, hidden, out, ws, *rest):
+        """Launch on the stream given last; bias1 and bias2 (device addresses) may come
+        before it (the EagleFFN form with biases)."""
+        if len(rest) == 1:
+            rc = run(plan_ref, x, w1, w2, hidden, out, ws, rest[0])
+        else:
+            b1, b2, stream = rest
+            rc = run_ex(plan_ref, x, w1, b1, w2, b2, hidden, out, ws, stream)
         if rc:
             _lib.check(rc)
 

@@ -31,10 +31,16 @@ class Problem:
     n: int
     dtype: str
     layout: str
+    activation: str = "gelu"   # gelu (the reference's operator), silu or swiglu
 
     @property
     def output_shape(self):
         return (*self.input_shape[:-1], self.n)
+
+    @property
+    def up_width(self):
+        """Rows of weight1: H, or 2H for SwiGLU (gate rows, then up rows)."""
+        return 2 * self.h if self.activation == "swiglu" else self.h
 
 
 def _shape(value, name, ranks):
@@ -46,8 +52,14 @@ def _shape(value, name, ranks):
     return result
 
 
-def problem_from_shapes(x_shape, w1_shape, w2_shape, dtype="float16", layout="linear"):
-    """Validate shapes (ops/host/inputs.py:38-53): X rank 2-8, W1 [H,K], W2 [N,H]."""
+ACTIVATIONS = ("gelu", "silu", "swiglu")
+
+
+def problem_from_shapes(x_shape, w1_shape, w2_shape, dtype="float16", layout="linear", activation="gelu"):
+    """Validate shapes (ops/host/inputs.py:38-53): X rank 2-8, W1 [H,K], W2 [N,H].
+
+    activation 'silu' keeps these shapes; 'swiglu' takes W1 [2H,K], gate rows then up rows
+    (the EagleFFN paths, spec/MindIE-SD EagleFFN算子实现分析.md:17-71, :76-86)."""
     x = _shape(x_shape, "x", range(2, 9))
     w1 = _shape(w1_shape, "weight1", (2,))
     w2 = _shape(w2_shape, "weight2", (2,))
@@ -55,25 +67,33 @@ def problem_from_shapes(x_shape, w1_shape, w2_shape, dtype="float16", layout="li
         raise ValueError("dtype must be float16 or bfloat16")
     if layout != "linear":
         raise ValueError("Only explicit layout='linear' is enabled in this implementation")
-    h, k = w1
-    n, h2 = w2
-    if x[-1] != k or h != h2:
-        raise ValueError("Expected x[..., K], weight1[H,K], weight2[N,H]")
+    if activation not in ACTIVATIONS:
+        raise ValueError(f"activation must be one of {ACTIVATIONS}")
+    u, k = w1
+    n, h = w2
+    if x[-1] != k or u != (2 * h if activation == "swiglu" else h):
+        raise ValueError("Expected x[..., K], weight1[2H,K], weight2[N,H]" if activation == "swiglu"
+                         else "Expected x[..., K], weight1[H,K], weight2[N,H]")
     if max(k, h, n) > MAX_DIM or prod(x[:-1]) > MAX_ROWS:
         raise ValueError("Shape exceeds the supported bounds (K, H, N <= 65535; M <= 2**31-16)")
-    return Problem(x, prod(x[:-1]), k, h, n, dtype, layout)
+    return Problem(x, prod(x[:-1]), k, h, n, dtype, layout, activation)
 
 
-def validate_tensors(x, weight1, weight2, layout="linear", require_device=False, require_npu=None):
+def validate_tensors(x, weight1, weight2, layout="linear", require_device=False, require_npu=None,
+                     activation="gelu", bias1=None, bias2=None):
     """Tensor checks of ops/host/inputs.py:56-71; `require_device` asks for ROCm GPU tensors.
 
     require_npu is the reference's name of the same switch (ops/host/inputs.py:56), accepted
-    so that its callers run unchanged; it asks for the device this build runs on."""
+    so that its callers run unchanged; it asks for the device this build runs on.  bias1
+    ([H], or [2H] for SwiGLU) and bias2 ([N]) are given together or not at all, like the
+    operands (same dtype and device, dense, no grad)."""
     import torch
     if require_npu is not None:
         require_device = bool(require_npu)
+    if (bias1 is None) != (bias2 is None):
+        raise ValueError("bias1 and bias2 must be given together or not at all")
 
-    tensors = (x, weight1, weight2)
+    tensors = (x, weight1, weight2) + (() if bias1 is None else (bias1, bias2))
     if any(not isinstance(t, torch.Tensor) for t in tensors):
         raise TypeError("x, weight1 and weight2 must be torch.Tensor")
     if any(t.dtype != x.dtype or t.device != x.device for t in tensors):
@@ -84,8 +104,11 @@ def validate_tensors(x, weight1, weight2, layout="linear", require_device=False,
         raise ValueError("Inference-only operator; detach inputs explicitly")
     if require_device and x.device.type != "cuda":
         raise ValueError("FFN execution requires ROCm GPU tensors; no torch fallback is used")
-    return problem_from_shapes(x.shape, weight1.shape, weight2.shape,
-                               str(x.dtype).removeprefix("torch."), layout)
+    p = problem_from_shapes(x.shape, weight1.shape, weight2.shape,
+                            str(x.dtype).removeprefix("torch."), layout, activation)
+    if bias1 is not None and (tuple(bias1.shape) != (p.up_width,) or tuple(bias2.shape) != (p.n,)):
+        raise ValueError(f"Expected bias1[{p.up_width}] and bias2[{p.n}]")
+    return p
 
 
 def _in_place(t, width):
@@ -103,7 +126,24 @@ def operands_aligned(x, weight1, weight2, plan):
             and weight1.is_contiguous() and weight2.is_contiguous())
 
 
-def prepare_storage(x, weight1, weight2, plan, alias_aligned=False):
+def interleave_gate_up(weight, h, hp):
+    """SwiGLU weight1 [2h, K] (gate rows, then up rows) or bias1 [2h] -> the [2hp, ...] layout the
+    up GEMM reads: 32-row blocks alternate, block 2b holding gate rows 32b..32b+31 and block 2b+1
+    the up rows of the same hidden columns; zero past h."""
+    import torch
+    tail = tuple(weight.shape[1:])
+    out = torch.zeros((hp // 32, 2, 32) + tail, device=weight.device, dtype=weight.dtype)
+    flat = out.view((hp // 32, 2 * 32) + tail)
+    gate = torch.zeros((hp,) + tail, device=weight.device, dtype=weight.dtype)
+    up = torch.zeros_like(gate)
+    gate[:h].copy_(weight[:h])
+    up[:h].copy_(weight[h:2 * h])
+    out[:, 0].copy_(gate.view((hp // 32, 32) + tail))
+    out[:, 1].copy_(up.view((hp // 32, 32) + tail))
+    return flat.reshape((2 * hp,) + tail)
+
+
+def prepare_storage(x, weight1, weight2, plan, alias_aligned=False, bias1=None, bias2=None):
     """Contiguise and zero-pad into [mp,kp], [hp,kp], [np,hp]; allocate hidden, out, workspace.
 
     Same buffers as ops/host/inputs.py:74-90; the FP32 workspace holds the partial tiles of
@@ -129,7 +169,12 @@ def prepare_storage(x, weight1, weight2, plan, alias_aligned=False):
         xs = torch.zeros((plan.mp, plan.kp), device=x.device, dtype=x.dtype)
         xs[:p.m, :p.k].copy_(x.reshape(p.m, p.k))
         ldx = plan.kp
-    if alias_aligned and _in_place(weight1, p.k):
+    if p.activation == "swiglu":
+        # always a copy: the gate and up rows are interleaved for the up GEMM
+        wk = torch.zeros((2 * p.h, plan.kp), device=x.device, dtype=x.dtype)
+        wk[:, :p.k].copy_(weight1)
+        w1s, ldw1 = interleave_gate_up(wk, p.h, plan.hp), plan.kp
+    elif alias_aligned and _in_place(weight1, p.k):
         w1s, ldw1 = weight1, p.k
     else:
         w1s = torch.zeros((plan.hp, plan.kp), device=x.device, dtype=x.dtype)
@@ -144,6 +189,12 @@ def prepare_storage(x, weight1, weight2, plan, alias_aligned=False):
     # the reduction runs to the logical K when both up operands hold whole chunks up to it
     k = p.k if p.k % 8 == 0 else plan.kp
     layout = (k, p.h, p.n, ldx, ldw1, ldw2)
-    return (xs, w1s, w2s, hidden, out, ws), layout
+    storage = (xs, w1s, w2s, hidden, out, ws)
+    if bias1 is not None:
+        # copies: 16-byte aligned; SwiGLU's bias1 interleaved like its weight rows
+        b1s = (interleave_gate_up(bias1, p.h, plan.hp) if p.activation == "swiglu"
+               else bias1.detach().clone().contiguous())
+        storage += (b1s, bias2.detach().clone().contiguous())
+    return storage, layout
 
 

@@ -81,6 +81,11 @@ class Plan:
     native: object = None
 
     @property
+    def activation(self):
+        """gelu (with the `gelu` form), silu or swiglu: the problem's activation."""
+        return self.problem.activation
+
+    @property
     def workspace_bytes(self):
         return self.workspace_shape[0] * self.workspace_shape[1] * 4
 
@@ -127,15 +132,19 @@ def make_plan(problem, selection=Selection(), block_num=DEFAULT_BLOCK_NUM, *, ge
     mp, kp = align(problem.m, 64), align(problem.k, 16)
     hp, np_ = align(problem.h, 64), align(problem.n, 64)
     dtype = _lib.BF16 if problem.dtype == "bfloat16" else _lib.FP16
+    activation = getattr(problem, "activation", "gelu")
     if tuned and up_variant is None and down_variant is None:
         from .. import tuning
+        # the key's epilogue field: the GELU form, or the other activation's name
+        epilogue = gelu if activation == "gelu" else activation
         hit = tuning.lookup(tuning.make_key(problem.m, mp, kp, hp, np_, problem.dtype,
-                                            selection.down_impl, gelu, block_num))
+                                            selection.down_impl, epilogue, block_num))
         if hit is not None:
             up_variant, down_variant = hit
     native = _lib.make_plan(mp, kp, hp, np_, dtype, selection.down_impl, gelu, block_num,
                             -1 if up_variant is None else up_variant,
-                            -1 if down_variant is None else down_variant, m=problem.m)
+                            -1 if down_variant is None else down_variant, m=problem.m,
+                            activation=activation)
     up = _tile(native.up_bm, native.up_bn, native.up_bk, native.up_variant)
     down = _tile(native.down_bm, native.down_bn, native.down_bk, native.down_variant)
     if native.workspace_bytes:   # Stream-K down and/or split up GEMM

@@ -34,9 +34,15 @@ extern "C" {
 #define FFN_MI355X_DOWN_FULL_LOAD_A 2 /* reported unavailable, no fallback */
 #define FFN_MI355X_DOWN_FULL_LOAD_B 3 /* reported unavailable, no fallback */
 
-/* GELU form applied in the up-projection epilogue */
+/* Activation of the up-projection epilogue.  The reference computes the GELU forms only; SiLU
+ * and SwiGLU are the other two paths of the EagleFFN operator its analysis describes
+ * (spec/MindIE-SD EagleFFN算子实现分析.md:17-71). */
 #define FFN_MI355X_GELU_ERF 0      /* 0.5*z*(1+erf(z/sqrt2)), F.gelu(approximate='none') */
 #define FFN_MI355X_GELU_RATIONAL 1 /* clamp + P5/Q5 rational erf, validation/reference.py:5-13 */
+#define FFN_MI355X_SILU 2          /* z/(1+exp(-z)) */
+#define FFN_MI355X_SWIGLU 3        /* SiLU(gate)*up: W1 holds 2*hp rows, gate and up rows interleaved
+                                      in 32-row blocks (rows 64b..64b+31 = gate rows 32b..32b+31,
+                                      rows 64b+32..64b+63 = up rows 32b..32b+31), zero past h */
 
 /* return codes */
 #define FFN_MI355X_OK 0
@@ -51,7 +57,7 @@ extern "C" {
 typedef struct ffn_mi355x_plan {
     int m;                       /* logical rows of X (rows m..mp-1 are zero padding) */
     int mp, kp, hp, np;          /* padded extents the plan was made for */
-    int dtype, down_impl, gelu;
+    int dtype, down_impl, activation; /* FFN_MI355X_GELU_ERF .. FFN_MI355X_SWIGLU */
     int block_num;               /* persistent workgroups per launch (<= CU count) */
     int up_variant, down_variant;
     int up_bm, up_bn, up_bk;     /* up-projection macro tile (M x H x K) */
@@ -99,7 +105,7 @@ int ffn_mi355x_query(int device, int* cu_count, char* arch, int arch_len);
  * m is the logical row count: the zero-padding rows of X and hidden are then
  * never fetched (they read as zeros), which matters for small-M decode shapes. */
 int ffn_mi355x_make_plan(int m, int mp, int kp, int hp, int np, int dtype, int down_impl,
-                         int gelu, int block_num, int up_variant, int down_variant,
+                         int activation, int block_num, int up_variant, int down_variant,
                          ffn_mi355x_plan* plan);
 
 /* Reads the operands in place at their logical widths instead of from buffers padded
@@ -141,6 +147,22 @@ int ffn_mi355x_run(const ffn_mi355x_plan* plan, const void* x, const void* w1,
  * Every partial is written before it is read within a call, so nothing needs clearing. */
 int ffn_mi355x_run_noalloc(const ffn_mi355x_plan* plan, const void* x, const void* w1,
                            const void* w2, void* hidden, void* out, void* hip_stream);
+
+/* ffn_mi355x_run with per-column biases, the EagleFFN form
+ *     Y = act(X . W1^T + b1) . W2^T + b2
+ * (spec/MindIE-SD EagleFFN算子实现分析.md:17-40; the reference operator has no bias).
+ * b1 holds h values (SwiGLU: 2*hp, interleaved like W1's rows), b2 holds n values, in the
+ * storage type; each is added in FP32 before the activation (b1) or the cast (b2).  Both or
+ * neither (FFN_MI355X_EINVAL otherwise); NULL, NULL is ffn_mi355x_run. */
+int ffn_mi355x_run_ex(const ffn_mi355x_plan* plan, const void* x, const void* w1, const void* b1,
+                      const void* w2, const void* b2, void* hidden, void* out, void* ws,
+                      void* hip_stream);
+
+/* The two stages of ffn_mi355x_run_ex alone (b1 / b2 may be NULL: no bias). */
+int ffn_mi355x_up_ex(const ffn_mi355x_plan* plan, const void* x, const void* w1, const void* b1,
+                     void* hidden, void* ws, void* hip_stream);
+int ffn_mi355x_down_ex(const ffn_mi355x_plan* plan, const void* hidden, const void* w2,
+                       const void* b2, void* out, void* ws, void* hip_stream);
 
 /* Stage 1 alone: up-projection with GELU epilogue (ops/kernel/ffn.py:207-360,
  * 540-581, the cube/vector up regions of both kernels).  `ws` holds

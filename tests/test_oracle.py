@@ -148,3 +148,63 @@ def test_row_sampling_equals_full():
     rows = torch.tensor([0, 5, 11, 15])
     full = ffn_torch(x, w1, w2).reshape(16, 16)
     assert torch.equal(ffn_rows(x, w1, w2, rows), full[rows])
+
+
+# ---- the EagleFFN paths (spec/MindIE-SD EagleFFN算子实现分析.md:17-71) ------------------------
+
+def test_silu_closed_form_and_identity():
+    """SiLU is z / (1 + e^-z) (math.exp in double), not z * tanh or the GELU; SiLU(z) - SiLU(-z) = z."""
+    from oracle.reference import silu
+    pts = [i / 8 for i in range(-96, 97)]
+    got = silu(torch.tensor(pts, dtype=torch.float32)).double()
+    for z, g in zip(pts, got.tolist()):
+        exact = z / (1 + math.exp(-z))
+        assert abs(g - exact) <= 2e-6 * max(1.0, abs(z)), z
+    z = torch.linspace(-20, 20, 801)
+    assert torch.allclose(silu(z) - silu(-z), z, atol=2e-5)
+    assert torch.allclose(silu(z), torch.nn.functional.silu(z), atol=1e-6, rtol=1e-6)
+    assert abs(silu(torch.tensor([1.0])).item() - gelu_erf(torch.tensor([1.0])).item()) > 1e-2
+
+
+def _brute_eagle(x, w1, w2, b1, b2, act):
+    """act(x W1^T + b1) W2^T + b2 in pure Python; act maps the list of up outputs of one row to
+    the hidden row (SwiGLU: the first half gated by the second)."""
+    out = []
+    for row in x:
+        z = [sum(a * b for a, b in zip(row, w)) + bb for w, bb in zip(w1, b1)]
+        hid = act(z)
+        out.append([sum(hh * w for hh, w in zip(hid, wr)) + bb for wr, bb in zip(w2, b2)])
+    return out
+
+
+@pytest.mark.parametrize("activation", ["gelu", "silu", "swiglu"])
+def test_ffn_torch_eagle_paths_brute_force(activation):
+    """Integer operands and biases: the bias goes into the up sum before the activation and into
+    the down sum before the cast; SwiGLU gates with the first H columns of the up output (swapping
+    the halves, or adding bias1 after the activation, changes the result)."""
+    g = torch.Generator().manual_seed(11)
+    m, k, h, n = 3, 5, 4, 2
+    u = 2 * h if activation == "swiglu" else h
+    x = torch.randint(-2, 3, (m, k), generator=g).float()
+    w1 = torch.randint(-2, 3, (u, k), generator=g).float()
+    w2 = torch.randint(-2, 3, (n, h), generator=g).float()
+    b1 = torch.randint(-2, 3, (u,), generator=g).float()
+    b2 = torch.randint(-2, 3, (n,), generator=g).float()
+    gelu1 = lambda v: 0.5 * v * (1 + math.erf(v / math.sqrt(2)))
+    silu1 = lambda v: v / (1 + math.exp(-v))
+    act = {"gelu": lambda z: [gelu1(v) for v in z], "silu": lambda z: [silu1(v) for v in z],
+           "swiglu": lambda z: [silu1(a) * b for a, b in zip(z[:h], z[h:])]}[activation]
+    want = torch.tensor(_brute_eagle(x.tolist(), w1.tolist(), w2.tolist(), b1.tolist(), b2.tolist(), act))
+    got = ffn_torch(x, w1, w2, activation=activation, bias1=b1, bias2=b2)
+    assert torch.allclose(got, want, atol=1e-4, rtol=1e-5)
+    # the slips this pins: no bias, bias after the activation, swapped SwiGLU halves
+    assert not torch.allclose(ffn_torch(x, w1, w2, activation=activation), want, atol=1e-3)
+    late = torch.tensor(_brute_eagle(x.tolist(), w1.tolist(), w2.tolist(), [0.0] * u, b2.tolist(),
+                                     lambda z: [a + b for a, b in zip(act(z), b1.tolist())]
+                                     if activation != "swiglu" else act(z)))
+    if activation != "swiglu":
+        assert not torch.allclose(got, late, atol=1e-3)
+    else:
+        swapped = ffn_torch(x, torch.cat([w1[h:], w1[:h]]), w2, activation=activation,
+                            bias1=torch.cat([b1[h:], b1[:h]]), bias2=b2)
+        assert not torch.allclose(swapped, want, atol=1e-3)
