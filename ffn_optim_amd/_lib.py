@@ -31,7 +31,8 @@ class PlanStruct(ctypes.Structure):
         "down_tiles", "down_grid", "down_k_iters", "down_dp_tiles",
         "down_sk_tiles", "down_slots_per_wg")] + [("workspace_bytes", ctypes.c_size_t)] + [
         (name, ctypes.c_int) for name in ("k", "h", "n", "ldx", "ldw1", "ldw2",
-                                          "up_k_iters", "up_sk_tiles", "up_slots_per_wg")] + [
+                                          "up_k_iters", "up_sk_tiles", "up_slots_per_wg",
+                                          "x_d1", "x_d2", "x_s0", "x_s1", "x_s2")] + [
         ("stamp", ctypes.c_ulonglong)]
 
     def to_dict(self):
@@ -46,6 +47,7 @@ SIGNATURES = {
     "ffn_mi355x_make_plan": (_i, [_i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _P(PlanStruct)]),
     "ffn_mi355x_workspace_bytes": (_i, [_P(PlanStruct), _P(ctypes.c_size_t)]),
     "ffn_mi355x_set_operands": (_i, [_P(PlanStruct), _i, _i, _i, _i, _i, _i]),
+    "ffn_mi355x_set_x_rows": (_i, [_P(PlanStruct), _i, _i, _i, _i, _i]),
     "ffn_mi355x_run": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ffn_mi355x_run_noalloc": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp]),
     "ffn_mi355x_run_ex": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
@@ -138,6 +140,11 @@ def make_plan(mp, kp, hp, np_, dtype, down_impl, gelu, block_num, up_variant=-1,
 def set_operands(plan: PlanStruct, k, h, n, ldx, ldw1, ldw2) -> None:
     """Point a native plan at operands of their logical widths (ffn_mi355x_set_operands)."""
     check(load().ffn_mi355x_set_operands(ctypes.byref(plan), k, h, n, ldx, ldw1, ldw2))
+
+
+def set_x_rows(plan: PlanStruct, d1, d2, s0, s1, s2) -> None:
+    """Read X as gathered rows of a strided view (ffn_mi355x_set_x_rows); d1 = 0 undoes it."""
+    check(load().ffn_mi355x_set_x_rows(ctypes.byref(plan), d1, d2, s0, s1, s2))
 
 
 def variants() -> list[dict]:

@@ -116,10 +116,12 @@ def prepare_ffn(x, weight1, weight2, *, up_impl="basic", down_impl="basic", bloc
         stream = torch.cuda.current_stream()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
-        storage, layout = prepare_storage(x, weight1, weight2, plan, alias_aligned=_alias,
-                                          bias1=bias1, bias2=bias2)
+        storage, layout, x_rows = prepare_storage(x, weight1, weight2, plan, alias_aligned=_alias,
+                                                  bias1=bias1, bias2=bias2)
         end.record()
         _lib.set_operands(plan.native, *layout)
+        if x_rows is not None:
+            _lib.set_x_rows(plan.native, *x_rows)
         end.synchronize()
         auxiliary_ms = start.elapsed_time(end)
         tensors = tuple(t.data_ptr() for t in storage)

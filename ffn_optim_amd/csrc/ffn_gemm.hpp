@@ -67,6 +67,11 @@ struct GemmParams {
     int c_cols;           // columns of C (N, or N / 2 for SwiGLU, whose column pairs make one output)
     const void* bias;     // per-column bias in the storage type, added in FP32 before the activation
     int bias_n;           // bias values present; columns at or past bias_n add zero (NULL bias: none)
+    // Gathered rows of A (a strided activation read in place): row r = (i0, i1, i2) in a
+    // [d0, a_d1, a_d2] grid starts at element i0*a_s0 + i1*a_s1 + i2*a_s2; K is contiguous and
+    // the rows lie within a_bytes of a.  a_gather = 0: row r starts at r*lda.
+    int a_gather, a_d1, a_d2, a_s0, a_s1, a_s2;
+    unsigned a_bytes;
 };
 
 // SYNCQ_: MFMA slot of a stage's last k-step after which the stage wait + barrier is placed
@@ -370,7 +375,7 @@ struct UnitWalker {
 // the GEMM engine
 // ---------------------------------------------------------------------------
 
-template <int DT, class C>
+template <int DT, class C, bool GA = false>
 struct Engine {
     static constexpr int FM = C::FM, FN = C::FN, NT = C::NT, S = C::STAGES, KS = C::KSTEPS;
     static_assert(KS % 2 == 0, "fragment double-buffer assumes an even number of k-steps per wave");
@@ -402,7 +407,9 @@ struct Engine {
         const char* abase = (const char*)p.a + (size_t)row0 * (size_t)lda2;
         const char* bbase = (const char*)p.b + (size_t)col0 * (size_t)ldb2;
         // zero-padding rows of A are not fetched: past m_valid the range check returns zeros
-        ra = make_rsrc(abase, (uint32_t)max(0, min(C::BM, p.m_valid - row0)) * (uint32_t)lda2);
+        // (gathered rows: the whole operand, rows past m_valid get the zero-fill offset)
+        if constexpr (GA) ra = make_rsrc(p.a, p.a_bytes);
+        else ra = make_rsrc(abase, (uint32_t)max(0, min(C::BM, p.m_valid - row0)) * (uint32_t)lda2);
         rb = make_rsrc(bbase, (uint32_t)max(0, min(C::BN, p.n_valid - col0)) * (uint32_t)ldb2);
     }
 
@@ -413,8 +420,9 @@ struct Engine {
     struct DmaLane {
         uint32_t a[C::NPAR], b[C::NPAR];
         int kk[C::NPAR];
+        uint32_t ga[GA ? C::A_PW : 1];  // gathered rows: byte offset of each A instruction's chunk
     };
-    __device__ __forceinline__ DmaLane dma_lane(const GemmParams& p) const {
+    __device__ __forceinline__ DmaLane dma_lane(const GemmParams& p, const Unit& u) const {
         // from an opaque lane id: the values depend only on the thread and would otherwise be
         // hoisted out of the persistent loop and held (spilled) across the epilogue
         int ln = lane;
@@ -427,6 +435,17 @@ struct Engine {
             d.kk[par] = kk;
             d.a[par] = (uint32_t)(rl * p.lda * 2 + kk * 2);
             d.b[par] = (uint32_t)(rl * p.ldb * 2 + kk * 2);
+        }
+        if constexpr (GA) {
+            // the row of each A instruction, decomposed over the gathered grid once per unit
+#pragma unroll
+            for (int D = 0; D < C::A_PW; ++D) {
+                const int r = u.tm * C::BM + (wave * C::A_PW + D) * C::RPB + rl;
+                const unsigned i2 = (unsigned)r % (unsigned)p.a_d2, t = (unsigned)r / (unsigned)p.a_d2;
+                const unsigned i1 = t % (unsigned)p.a_d1, i0 = t / (unsigned)p.a_d1;
+                const unsigned e = i0 * (unsigned)p.a_s0 + i1 * (unsigned)p.a_s1 + i2 * (unsigned)p.a_s2;
+                d.ga[D] = r < p.m_valid ? e * 2u + (unsigned)d.kk[D % C::NPAR] * 2u : 0x80000000u;
+            }
         }
         return d;
     }
@@ -456,8 +475,11 @@ struct Engine {
         if constexpr (D < C::A_PW) {
             const int blk = wave * C::A_PW + D;
             constexpr int par = D % C::NPAR;
+            // (a gathered row past m_valid already holds the zero-fill offset; adding the K
+            // offset keeps it at or past 2^31)
             const uint32_t off = L.kk[par] < t.lim
-                                     ? L.a[par] + (uint32_t)blk * (uint32_t)(C::RPB * p.lda * 2) + t.k0x2
+                                     ? (GA ? L.ga[GA ? D : 0] + t.k0x2
+                                           : L.a[par] + (uint32_t)blk * (uint32_t)(C::RPB * p.lda * 2) + t.k0x2)
                                      : 0x80000000u;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 ra, (__attribute__((address_space(3))) void*)(st + blk * 1024), 16, (int)off, 0, 0, 0);
@@ -500,14 +522,21 @@ struct Engine {
     }
 
     template <bool FAST, int D0, int D1>
-    __device__ __forceinline__ void issue_range(const GemmParams& p, const __amdgpu_buffer_rsrc_t& ra,
+    __device__ __forceinline__ void issue_range_impl(const GemmParams& p, const __amdgpu_buffer_rsrc_t& ra,
                                                 const __amdgpu_buffer_rsrc_t& rb, int stage,
                                                 const DmaLane& L, const DmaIt& t) const {
         if constexpr (D0 < D1) {
             if constexpr (FAST) issue_one_fast<D0>(p, ra, rb, stage, L, t);
             else issue_one<D0>(p, ra, rb, stage, L, t);
-            issue_range<FAST, D0 + 1, D1>(p, ra, rb, stage, L, t);
+            issue_range_impl<FAST, D0 + 1, D1>(p, ra, rb, stage, L, t);
         }
+    }
+    // (gathered rows always take the checked path: the host launches them without FASTK)
+    template <bool FAST, int D0, int D1>
+    __device__ __forceinline__ void issue_range(const GemmParams& p, const __amdgpu_buffer_rsrc_t& ra,
+                                                const __amdgpu_buffer_rsrc_t& rb, int stage,
+                                                const DmaLane& L, const DmaIt& t) const {
+        issue_range_impl<FAST && !GA, D0, D1>(p, ra, rb, stage, L, t);
     }
 
     // K-iterations 0..S-2 of a unit go to stages 0..S-2; iteration S-1+it is fetched during
@@ -519,7 +548,7 @@ struct Engine {
     __device__ __forceinline__ void prologue(const GemmParams& p, const Unit& u) const {
         __amdgpu_buffer_rsrc_t ra, rb;
         rsrc(p, u, ra, rb);
-        const DmaLane L = dma_lane(p);
+        const DmaLane L = dma_lane(p, u);
 #pragma unroll
         for (int s = 0; s < S - 1; ++s)
             issue_range<false, 0, C::LOADS>(p, ra, rb, s, L, dma_it(p, u.kb + s, u.kb + s < u.ke));
@@ -704,7 +733,7 @@ struct Engine {
             for (int i = 0; i < FM; ++i) acc[j][i] = f32x16{};
         __amdgpu_buffer_rsrc_t ra, rb;
         rsrc(p, u, ra, rb);
-        const DmaLane L = dma_lane(p);
+        const DmaLane L = dma_lane(p, u);
         const int n = u.ke - u.kb;
         wait_vmcnt<0>();
         barrier();
@@ -1051,7 +1080,7 @@ struct Engine {
 // Persistent GEMM: every workgroup walks its units (whole tiles, then for Stream-K its split
 // iterations) with the DMA of the next unit overlapping the epilogue of the current one.
 // Split pieces that share a tile publish FP32 partials; ffn_sk_reduce_kernel finishes them.
-template <int DT, class C, int EPI, bool SK, bool FASTK>
+template <int DT, class C, int EPI, bool SK, bool FASTK, bool GATHER = false>
 __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
     // The activation epilogue stores from registers, where its VALU work overlaps the stores;
     // the plain cast stages through LDS, whose full-row stores drain faster when every
@@ -1063,7 +1092,8 @@ __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
     constexpr bool EPI_IN_REGS = EPI != EPI_STORE || SK;
     constexpr int SMEM = C::WGK > 1 ? C::LDS_USE : EPI_IN_REGS ? C::LDS_BYTES : C::LDS_ALLOC;
     __shared__ __attribute__((aligned(1024))) char smem_raw[SMEM];
-    Engine<DT, C> eng((lds_char*)smem_raw, p);
+    static_assert(!(GATHER && FASTK), "gathered rows take the checked refill path");
+    Engine<DT, C, GATHER> eng((lds_char*)smem_raw, p);
     f32x16 acc[C::FN][C::FM];
 
     const int G = gridDim.x;

@@ -30,6 +30,13 @@ namespace {
 // one launch of ffn_gemm_kernel with the DMA addressing the plan chose
 template <class CFG, int EPI, bool SK>
 void launch_gemm(const ffn::GemmParams* p, dim3 g, dim3 b, hipStream_t stream) {
+    if constexpr (EPI != ffn::EPI_STORE || SK) {
+        // up roles (and the split GEMM, which a split up uses) may read gathered activation rows
+        if (p->a_gather) {
+            hipLaunchKernelGGL((ffn::ffn_gemm_kernel<FFN_DT, CFG, EPI, SK, false, true>), g, b, 0, stream, *p);
+            return;
+        }
+    }
     if (p->fast_dma)
         hipLaunchKernelGGL((ffn::ffn_gemm_kernel<FFN_DT, CFG, EPI, SK, true>), g, b, 0, stream, *p);
     else

@@ -280,10 +280,24 @@ constexpr int kMaxPitch = 4000000;
 
 bool pitch_ok(int ld) { return ld % 8 == 0 && ld <= kMaxPitch; }
 
+// Bytes from X's base to the end of the furthest row element the up GEMM reads, for gathered
+// rows (ffn_mi355x_set_x_rows); -1 for a grid that does not tile the m rows.
+long long x_grid_span(const ffn_mi355x_plan* p) {
+    if (p->x_d1 < 1 || p->x_d2 < 1 || p->m % ((long long)p->x_d1 * p->x_d2) != 0) return -1;
+    if (p->x_s0 < 0 || p->x_s1 < 0 || p->x_s2 < 0 || p->x_s0 % 8 || p->x_s1 % 8 || p->x_s2 % 8) return -1;
+    const long long d0 = p->m / ((long long)p->x_d1 * p->x_d2);
+    return ((d0 - 1) * p->x_s0 + (long long)(p->x_d1 - 1) * p->x_s1 + (long long)(p->x_d2 - 1) * p->x_s2 + p->k) * 2;
+}
+
+// Gathered rows are addressed with 32-bit buffer offsets below 2^31, the zero-fill offset.
+constexpr long long kMaxGatherSpan = 1LL << 31;
+
 bool layout_ok(const ffn_mi355x_plan* p) {
+    const bool x_ok = p->x_d1 == 0 ? p->x_d2 == 0 && p->x_s0 == 0 && p->x_s1 == 0 && p->x_s2 == 0
+                                   : x_grid_span(p) > 0 && x_grid_span(p) <= kMaxGatherSpan;
     return p->k >= 1 && p->k <= p->kp && (p->k % 8 == 0 || p->k == p->kp) && p->h >= 1 && p->h <= p->hp &&
            p->n >= 1 && p->n <= p->np && p->ldx >= p->k && pitch_ok(p->ldx) && p->ldw1 >= p->k &&
-           pitch_ok(p->ldw1) && p->ldw2 >= down_depth(p) && pitch_ok(p->ldw2);
+           pitch_ok(p->ldw1) && p->ldw2 >= down_depth(p) && pitch_ok(p->ldw2) && x_ok;
 }
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
@@ -331,7 +345,8 @@ unsigned long long plan_stamp(const ffn_mi355x_plan* p) {
                         p->up_variant, p->down_variant, p->up_bm, p->up_bn, p->up_bk, p->down_bm, p->down_bn,
                         p->down_bk, p->up_tiles, p->up_grid, p->down_tiles, p->down_grid, p->down_k_iters,
                         p->down_dp_tiles, p->down_sk_tiles, p->down_slots_per_wg, p->k, p->h, p->n, p->ldx,
-                        p->ldw1, p->ldw2, p->up_k_iters, p->up_sk_tiles, p->up_slots_per_wg};
+                        p->ldw1, p->ldw2, p->up_k_iters, p->up_sk_tiles, p->up_slots_per_wg,
+                        p->x_d1, p->x_d2, p->x_s0, p->x_s1, p->x_s2};
     for (int v : ints) mix((unsigned long long)(unsigned)v);
     mix((unsigned long long)p->workspace_bytes);
     return h;
@@ -480,6 +495,7 @@ int ffn_mi355x_make_plan(int m, int mp, int kp, int hp, int np, int dtype, int d
     if (up_ws > plan->workspace_bytes) plan->workspace_bytes = up_ws;
     plan->k = kp, plan->h = hp, plan->n = np;
     plan->ldx = kp, plan->ldw1 = kp, plan->ldw2 = hp;
+    plan->x_d1 = plan->x_d2 = plan->x_s0 = plan->x_s1 = plan->x_s2 = 0;
     if (!layout_ok(plan))
         return fail(FFN_MI355X_EINVAL, "padded extents exceed the largest row pitch (%d elements)", kMaxPitch);
     plan->stamp = plan_stamp(plan);
@@ -497,6 +513,22 @@ int ffn_mi355x_set_operands(ffn_mi355x_plan* plan, int k, int h, int n, int ldx,
                     "(kp=%d hp=%d np=%d): k a multiple of 8 or kp, pitches multiples of 8 covering "
                     "the widths and at most %d, W2 spanning hp columns when h is not a multiple of 8",
                     k, h, n, ldx, ldw1, ldw2, plan->kp, plan->hp, plan->np, kMaxPitch);
+    t.stamp = plan_stamp(&t);
+    *plan = t;
+    return ok();
+}
+
+int ffn_mi355x_set_x_rows(ffn_mi355x_plan* plan, int d1, int d2, int s0, int s1, int s2) {
+    if (!plan) return fail(FFN_MI355X_EINVAL, "plan must not be NULL");
+    if (!valid_plan(plan)) return fail(FFN_MI355X_EINVAL, "invalid plan");
+    ffn_mi355x_plan t = *plan;
+    if (d1 == 0) t.x_d1 = t.x_d2 = t.x_s0 = t.x_s1 = t.x_s2 = 0;
+    else t.x_d1 = d1, t.x_d2 = d2, t.x_s0 = s0, t.x_s1 = s1, t.x_s2 = s2;
+    if (!layout_ok(&t))
+        return fail(FFN_MI355X_EINVAL,
+                    "row grid d1=%d d2=%d strides (%d, %d, %d) does not fit m=%d k=%d: d1*d2 must divide m, "
+                    "strides be non-negative multiples of 8 and the rows lie within 2^31 bytes",
+                    d1, d2, s0, s1, s2, plan->m, plan->k);
     t.stamp = plan_stamp(&t);
     *plan = t;
     return ok();
@@ -529,7 +561,9 @@ int run_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, const voi
         return fail(FFN_MI355X_EINVAL, "the split up GEMM needs a workspace of %zu bytes", plan->workspace_bytes);
     const long long rows = w1_rows(plan);
     int rc;
-    if ((rc = check_span("x", x, span_bytes(plan->m, plan->ldx, plan->k))) != FFN_MI355X_OK ||
+    const bool gather = plan->x_d1 != 0;
+    const size_t x_span = gather ? (size_t)x_grid_span(plan) : span_bytes(plan->m, plan->ldx, plan->k);
+    if ((rc = check_span("x", x, x_span)) != FFN_MI355X_OK ||
         (rc = check_span("w1", w1, span_bytes(rows, plan->ldw1, plan->k))) != FFN_MI355X_OK ||
         (b1 && (rc = check_span("bias1", b1, (size_t)rows * 2u)) != FFN_MI355X_OK) ||
         (rc = check_span("hidden", hidden, span_bytes(plan->mp, plan->hp, plan->hp))) != FFN_MI355X_OK ||
@@ -552,6 +586,12 @@ int run_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, const voi
     gp.group_m = group_m_for(gp.tiles_m);
     gp.fast_dma = fast_dma_for(gp.K);
     gp.bias = b1, gp.bias_n = b1 ? (int)rows : 0;
+    if (gather) {
+        gp.a_gather = 1;
+        gp.a_d1 = plan->x_d1, gp.a_d2 = plan->x_d2;
+        gp.a_s0 = plan->x_s0, gp.a_s1 = plan->x_s1, gp.a_s2 = plan->x_s2;
+        gp.a_bytes = (unsigned)x_span;
+    }
     if (split) {
         // every tile split (no whole tiles): FP32 partials, then the fixup with the activation
         const long long total = (long long)plan->up_sk_tiles * plan->up_k_iters;

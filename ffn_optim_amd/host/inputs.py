@@ -117,6 +117,46 @@ def _in_place(t, width):
     return t.is_contiguous() and width % 8 == 0 and t.data_ptr() % 16 == 0
 
 
+# Gathered rows are addressed with 32-bit byte offsets below 2^31 (ffn_mi355x_set_x_rows).
+MAX_GATHER_SPAN = 2 ** 31
+
+
+def row_grid(x, k):
+    """How the up GEMM can read X [..., k] where it lies, as rows of k contiguous elements.
+
+    Leading dims of size 1 are dropped and neighbours whose strides chain (outer stride =
+    inner size * inner stride) are merged.  Returns ("pitch", ldx) when one dim is left (a
+    contiguous X or one sliced from wider rows: rows at one pitch), ("grid", (d1, d2, s0, s1,
+    s2)) when two or three are left (a permuted view such as a [B, S, K] tensor read as
+    [S, B, K]: row (i0, i1, i2) of a [m / (d1*d2), d1, d2] grid starts at i0*s0 + i1*s1 + i2*s2),
+    or None when the view must be copied: K not contiguous or not a multiple of 8, a stride or
+    the base off a 16-byte boundary, more than three dims left, or rows spread over 2^31 bytes
+    or more.  No counterpart in the reference, which copies every X (ops/host/inputs.py:74-90).
+    """
+    if k % 8 != 0 or x.stride(-1) != 1 or (x.data_ptr() % 16) != 0:
+        return None
+    dims = [(n, st) for n, st in zip(x.shape[:-1], x.stride()[:-1]) if n != 1]
+    merged = []
+    for n, st in reversed(dims):
+        if merged and st == merged[-1][0] * merged[-1][1]:
+            merged[-1] = (n * merged[-1][0], merged[-1][1])
+        else:
+            merged.append((n, st))
+    merged.reverse()
+    if any(st % 8 != 0 for _, st in merged) or len(merged) > 3:
+        return None
+    if not merged:
+        return ("pitch", k)
+    span = (sum((n - 1) * st for n, st in merged) + k) * x.element_size()
+    if span > MAX_GATHER_SPAN:
+        return None
+    if len(merged) == 1 and merged[0][1] >= k:
+        return ("pitch", merged[0][1])
+    merged = [(1, 0)] * (3 - len(merged)) + merged
+    (_, s0), (d1, s1), (d2, s2) = merged
+    return ("grid", (d1, d2, s0, s1, s2))
+
+
 def operands_aligned(x, weight1, weight2, plan):
     """True when X, W1 and W2 can all be used in place at the padded widths: contiguous, K,
     H and N already at their padded extents.  M needs no padding: the kernels never read
@@ -148,13 +188,16 @@ def prepare_storage(x, weight1, weight2, plan, alias_aligned=False, bias1=None, 
 
     Same buffers as ops/host/inputs.py:74-90; the FP32 workspace holds the partial tiles of
     the Stream-K down and of a split up GEMM (every slot is written before it is read).
-    Returns the six buffers and
-    the operand layout (k, h, n, ldx, ldw1, ldw2) for ffn_mi355x_set_operands.
+    Returns the six buffers, the operand layout (k, h, n, ldx, ldw1, ldw2) for
+    ffn_mi355x_set_operands and X's row grid (d1, d2, s0, s1, s2) for ffn_mi355x_set_x_rows,
+    or None when X is read as rows at pitch ldx.
 
-    With alias_aligned, every operand the kernels can read where it lies (_in_place) is
-    the caller's tensor itself, at its logical width, and only the others are copied:
-    for a launch that runs before the caller can modify them.  X needs K % 8 == 0, W1 the
-    same, W2 H % 8 == 0; a non-contiguous operand (a transposed view) is always copied.
+    With alias_aligned, every operand the kernels can read where it lies is the caller's
+    tensor itself, at its logical width, and only the others are copied: for a launch that
+    runs before the caller can modify them.  X needs K % 8 == 0 and K contiguous, and is read
+    in place even as a permuted or sliced view (row_grid); W1 needs K % 8 == 0 and W2
+    H % 8 == 0, both contiguous (a transposed weight is copied).  X read in place is kept as
+    an [m, k] view at pitch ldx, or as the caller's tensor itself when its rows form a grid.
     """
     import torch
 
@@ -162,9 +205,13 @@ def prepare_storage(x, weight1, weight2, plan, alias_aligned=False, bias1=None, 
     hidden = torch.empty((plan.mp, plan.hp), device=x.device, dtype=x.dtype)
     out = torch.empty((plan.mp, plan.np), device=x.device, dtype=x.dtype)
     ws = torch.empty(plan.workspace_shape, device=x.device, dtype=torch.float32)
-    xv = x.reshape(p.m, p.k) if x.is_contiguous() else None
-    if alias_aligned and xv is not None and _in_place(xv, p.k):
-        xs, ldx = xv, p.k
+    grid = row_grid(x, p.k) if alias_aligned else None
+    x_rows = None
+    if grid is not None and grid[0] == "pitch":
+        ldx = grid[1]
+        xs = x.as_strided((p.m, p.k), (ldx, 1))
+    elif grid is not None:
+        xs, ldx, x_rows = x, p.k, grid[1]
     else:
         xs = torch.zeros((plan.mp, plan.kp), device=x.device, dtype=x.dtype)
         xs[:p.m, :p.k].copy_(x.reshape(p.m, p.k))
@@ -195,6 +242,6 @@ def prepare_storage(x, weight1, weight2, plan, alias_aligned=False, bias1=None, 
         b1s = (interleave_gate_up(bias1, p.h, plan.hp) if p.activation == "swiglu"
                else bias1.detach().clone().contiguous())
         storage += (b1s, bias2.detach().clone().contiguous())
-    return storage, layout
+    return storage, layout, x_rows
 
 

@@ -84,6 +84,9 @@ typedef struct ffn_mi355x_plan {
     int up_k_iters;              /* BK-deep iterations along K per up tile */
     int up_sk_tiles;             /* up tiles split along K (0 or up_tiles) */
     int up_slots_per_wg;         /* FP32 partial-tile slots per workgroup of the split up */
+    /* Gathered rows of X (ffn_mi355x_set_x_rows): x_d1 = 0 reads row r at r * ldx; otherwise
+       row r = (i0 * x_d1 + i1) * x_d2 + i2 starts at element i0*x_s0 + i1*x_s1 + i2*x_s2. */
+    int x_d1, x_d2, x_s0, x_s1, x_s2;
     /* Check word over every field above, written by ffn_mi355x_make_plan and
        ffn_mi355x_set_operands.  The run entry points refuse a plan whose fields no longer
        match it (EINVAL "invalid plan"): its grids, tile counts and workspace size decide
@@ -117,6 +120,17 @@ int ffn_mi355x_make_plan(int m, int mp, int kp, int hp, int np, int dtype, int d
  * columns (ldw2 >= hp, zero past h).  No counterpart in the reference, whose prepare step
  * always copies into padded buffers (ops/host/inputs.py:74-90).  EINVAL on a bad layout. */
 int ffn_mi355x_set_operands(ffn_mi355x_plan* plan, int k, int h, int n, int ldx, int ldw1, int ldw2);
+
+/* Reads X in place as a strided view instead of rows at one pitch: the plan's m rows form a
+ * [m / (d1*d2), d1, d2] grid, row (i0, i1, i2) holding k contiguous elements from element
+ * i0*s0 + i1*s1 + i2*s2 of x.  This is how a permuted activation (the Canonical layout's
+ * transposed view, a [B, S, D] tensor read as [S, B, D]) is consumed without the copy the
+ * reference's prepare step makes (ops/host/inputs.py:74-90: x.contiguous() into [mp, kp]).
+ * d1, d2 >= 1 dividing m; strides >= 0 and multiples of 8 elements (16-byte rows); the
+ * furthest element read, ((m/(d1*d2)-1)*s0 + (d1-1)*s1 + (d2-1)*s2 + k) * 2 bytes from x,
+ * below 2^31.  d1 = 0 restores rows at pitch ldx.  Kept by ffn_mi355x_set_operands; EINVAL
+ * on a bad grid, plan unchanged. */
+int ffn_mi355x_set_x_rows(ffn_mi355x_plan* plan, int d1, int d2, int s0, int s1, int s2);
 
 /* Workspace bytes a plan needs (0 for the Basic down). */
 int ffn_mi355x_workspace_bytes(const ffn_mi355x_plan* plan, size_t* bytes);

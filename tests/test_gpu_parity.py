@@ -445,3 +445,50 @@ def test_buffers_outside_their_allocation_are_refused():
     say("host x:", rc, _lib.last_error())
     assert rc == -1 and "buffer x" in _lib.last_error()
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("case_id,x_rows", [("c3_unaligned_fp16", (5, 67, 335000, 1000, 5000))])
+def test_one_shot_ffn_reads_permuted_x_in_place(case_id, x_rows):
+    """ffn() on the unaligned 4-D workload's X, a [3, 5, 67, 1000] view with dims 1 and 2 of its
+    buffer swapped, reads the rows where they lie (a [201, 5, 67] row grid) instead of copying
+    them; results are bit-identical to the prepared (copied) path and pass the criterion."""
+    from ffn_optim_amd import ffn
+    from ffn_optim_amd.host.inputs import row_grid
+    case = get_case(case_id)
+    x, w1, w2 = make_inputs(case, "cuda")
+    assert not x.is_contiguous() and row_grid(x, x.shape[-1]) == ("grid", x_rows)
+    for down in ("basic", "streamk"):
+        say(case_id, "permuted X in place", down)
+        ref = prepare_ffn(x, w1, w2, down_impl=down).run().clone()
+        y = ffn(x, w1, w2, down_impl=down)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), down
+        assert_parity(y, x, w1, w2, tag=f"{case_id} {down} gathered X")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gathered_x_every_variant(dtype):
+    """The gathered-row form of the up GEMM for every compiled tile, forced: X is a permuted
+    [24, 9, 328] view of a [9, 24, 328] buffer (M=216, ragged for every tile; K=328 not a multiple
+    of any BK), and a shallow-M deep-K view whose up GEMM is split along K.  Bit-identical to the
+    same tiles on a contiguous copy."""
+    from ffn_optim_amd import ffn
+    g = torch.Generator().manual_seed(35)
+    shapes = (((9, 24, 328), 392, 264), ((4, 2, 8192), 256, 64))
+    for (d0, d1, k), h, n in shapes:
+        base = torch.randn(d0, d1, k, generator=g).to(dtype).cuda()
+        x = base.transpose(0, 1)
+        w1 = (torch.randn(h, k, generator=g) * k ** -0.5).to(dtype).cuda()
+        w2 = (torch.randn(n, h, generator=g) * h ** -0.5).to(dtype).cuda()
+        xc = x.contiguous()
+        variants = range(_lib.load().ffn_mi355x_num_variants()) if k == 328 else [None]
+        for v in variants:
+            say("gathered X", dtype, (d1, d0, k), h, n, "up variant", v)
+            prepared = prepare_ffn(xc, w1, w2, up_variant=v)
+            if k != 328:
+                assert prepared.plan.native.up_sk_tiles > 0   # the split up GEMM reads the grid too
+            ref = prepared.run().clone()
+            y = ffn(x, w1, w2, up_variant=v)
+            torch.cuda.synchronize()
+            assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), v
+        assert_parity(y, x, w1, w2, tag=f"gathered X {dtype} {(d1, d0, k)}")

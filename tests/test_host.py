@@ -32,7 +32,7 @@ def test_ranks_and_padding():
             w2 = torch.randn(23, 38).to(dtype)[:, ::2]
             p = validate_tensors(x, w1, w2)
             plan = make_plan(p)
-            (xp, a, b, hidden, out, ws), layout = prepare_storage(x, w1, w2, plan)
+            (xp, a, b, hidden, out, ws), layout, x_rows = prepare_storage(x, w1, w2, plan)
             assert layout == (p.k if p.k % 8 == 0 else plan.kp, p.h, p.n, plan.kp, plan.kp, plan.hp)
             assert xp.shape == (plan.mp, plan.kp) and a.shape == (plan.hp, plan.kp)
             assert b.shape == (plan.np, plan.hp) and hidden.shape == (plan.mp, plan.hp)
@@ -280,12 +280,12 @@ def test_operands_used_in_place_only_when_asked():
     w1, w2 = torch.randn(256, 128, generator=g).half(), torch.randn(64, 256, generator=g).half()
     plan = make_plan(problem_from_shapes(x.shape, w1.shape, w2.shape, "float16"), Selection(), 8)
     assert operands_aligned(x, w1, w2, plan)
-    (xs, w1s, w2s, hid, out, ws), layout = prepare_storage(x, w1, w2, plan, alias_aligned=True)
+    (xs, w1s, w2s, hid, out, ws), layout, x_rows = prepare_storage(x, w1, w2, plan, alias_aligned=True)
     assert xs.data_ptr() == x.data_ptr() and xs.shape == (100, 128)
     assert w1s is w1 and w2s is w2 and layout == (128, 256, 64, 128, 128, 256)
     assert hid.shape == (128, 256) and out.shape == (128, 64)
     # without the request the storage is a padded snapshot
-    (xs, w1s, _, _, _, _), layout = prepare_storage(x, w1, w2, plan)
+    (xs, w1s, _, _, _, _), layout, x_rows = prepare_storage(x, w1, w2, plan)
     assert xs.data_ptr() != x.data_ptr() and xs.shape == (128, 128)
     assert torch.equal(xs[:100], x.view(100, 128)) and not xs[100:].any()
     assert layout == (128, 256, 64, plan.kp, plan.kp, plan.hp)
@@ -294,22 +294,101 @@ def test_operands_used_in_place_only_when_asked():
     w12, w22 = torch.randn(200, 120, generator=g).half(), torch.randn(72, 200, generator=g).half()
     p2 = make_plan(problem_from_shapes(x2.shape, w12.shape, w22.shape, "float16"), Selection(), 8)
     assert not operands_aligned(x2, w12, w22, p2)
-    (xs, w1s, w2s, _, _, _), layout = prepare_storage(x2, w12, w22, p2, alias_aligned=True)
+    (xs, w1s, w2s, _, _, _), layout, _ = prepare_storage(x2, w12, w22, p2, alias_aligned=True)
     assert xs.data_ptr() == x2.data_ptr() and w1s is w12 and w2s is w22
     assert layout == (120, 200, 72, 120, 120, 200)
     # H not a multiple of 8: W2 is copied into [np, hp]; W1 [h, k] stays in place
     w13, w23 = torch.randn(201, 120, generator=g).half(), torch.randn(72, 201, generator=g).half()
     p3 = make_plan(problem_from_shapes(x2.shape, w13.shape, w23.shape, "float16"), Selection(), 8)
-    (xs, w1s, w2s, _, _, _), layout = prepare_storage(x2, w13, w23, p3, alias_aligned=True)
+    (xs, w1s, w2s, _, _, _), layout, _ = prepare_storage(x2, w13, w23, p3, alias_aligned=True)
     assert w1s is w13 and w2s.shape == (p3.np, p3.hp) and not w2s[:, 201:].any()
     assert layout == (120, 201, 72, 120, 120, p3.hp)
-    # K not a multiple of 8, or a non-contiguous X: copied and padded
+    # K not a multiple of 8, or K not contiguous: copied and padded
     for xx, ww1 in ((torch.randn(100, 100, generator=g).half(), torch.randn(256, 100, generator=g).half()),
-                    (x.transpose(0, 1), w1)):
+                    (torch.randn(128, 100, generator=g).half().t(), w1)):
         p = make_plan(problem_from_shapes(xx.shape, ww1.shape, w2.shape, "float16"), Selection(), 8)
-        (xs, w1s, _, _, _, _), layout = prepare_storage(xx, ww1, w2, p, alias_aligned=True)
-        assert xs.data_ptr() != xx.data_ptr() and xs.shape == (p.mp, p.kp)
+        (xs, w1s, _, _, _, _), layout, x_rows = prepare_storage(xx, ww1, w2, p, alias_aligned=True)
+        assert xs.data_ptr() != xx.data_ptr() and xs.shape == (p.mp, p.kp) and x_rows is None
         assert layout[3] == p.kp and (layout[0] == p.kp or xx.shape[-1] % 8 == 0)
+    # a permuted X [25, 4, 128] of a [4, 25, 128] tensor: read in place as a row grid
+    xt = x.transpose(0, 1)
+    p = make_plan(problem_from_shapes(xt.shape, w1.shape, w2.shape, "float16"), Selection(), 8)
+    (xs, _, _, _, _, _), layout, x_rows = prepare_storage(xt, w1, w2, p, alias_aligned=True)
+    assert xs is xt and layout[3] == 128 and x_rows == (25, 4, 0, 128, 3200)
+    # the same permuted X without the request: a padded snapshot
+    (xs, _, _, _, _, _), layout, x_rows = prepare_storage(xt, w1, w2, p)
+    assert xs.shape == (p.mp, p.kp) and x_rows is None and torch.equal(xs[:100], xt.reshape(100, 128))
+
+
+def _rows_of(x, grid):
+    """Gather the rows of X that a row_grid result addresses (the kernels' row addressing, on
+    the CPU): row r of the [m / (d1*d2), d1, d2] grid at element i0*s0 + i1*s1 + i2*s2."""
+    k = x.shape[-1]
+    flat = torch.as_strided(x, (x.untyped_storage().nbytes() // x.element_size(),), (1,), 0)
+    base = x.storage_offset()
+    m = x.numel() // k
+    if grid[0] == "pitch":
+        starts = [base + r * grid[1] for r in range(m)]
+    else:
+        d1, d2, s0, s1, s2 = grid[1]
+        starts = [base + (r // (d1 * d2)) * s0 + (r // d2 % d1) * s1 + (r % d2) * s2 for r in range(m)]
+    return torch.stack([flat[s:s + k] for s in starts])
+
+
+def test_row_grid_addresses_every_row():
+    """row_grid: the rows it addresses are X.reshape(m, k) row for row, for contiguous, sliced,
+    permuted and broadcast views; views it cannot address are refused (None)."""
+    from ffn_optim_amd.host.inputs import row_grid
+    base = torch.arange(2 * 3 * 5 * 7 * 64, dtype=torch.float32).half().view(2, 3, 5, 7, 64)
+    views = {
+        "contiguous": base.reshape(210, 64),
+        "rank5": base,
+        "sliced K": base.reshape(210, 64)[:, :32],
+        "permuted": base.permute(1, 0, 2, 3, 4),
+        "three groups": base.reshape(6, 5, 7, 64).permute(1, 0, 2, 3),
+        "canonical": base.reshape(6, 35, 64).transpose(0, 1),
+        "size-1 dims": base[:1, :1].permute(1, 0, 2, 3, 4),
+        "row step": base.reshape(210, 64)[::2],
+        "broadcast rows": base[0, 0, 0, :1].expand(9, 64),
+    }
+    want = {"contiguous": "pitch", "rank5": "pitch", "sliced K": "pitch", "permuted": "grid",
+            "three groups": "grid", "canonical": "grid", "size-1 dims": "pitch",
+            "row step": "pitch", "broadcast rows": "grid"}
+    for name, v in views.items():
+        grid = row_grid(v, v.shape[-1])
+        assert grid is not None and grid[0] == want[name], (name, grid)
+        assert torch.equal(_rows_of(v, grid), v.reshape(-1, v.shape[-1])), name
+    refused = {
+        "K strided": base.reshape(210, 64)[:, ::2],
+        "K not a multiple of 8": base.reshape(210, 64)[:, :36],
+        "four groups": base.permute(3, 2, 1, 0, 4),
+        "off 16 bytes": base.reshape(210, 64)[:, 4:36],
+        "K transposed": base.reshape(210, 64).t(),
+    }
+    for name, v in refused.items():
+        assert row_grid(v, v.shape[-1]) is None, name
+
+
+def test_set_x_rows_validates_grid():
+    """ffn_mi355x_set_x_rows accepts a grid that tiles m with 16-byte strides, keeps it through
+    set_operands, and rejects the rest without touching the plan."""
+    from ffn_optim_amd import _lib
+    plan = _lib.make_plan(1024, 1008, 1024, 1024, _lib.FP16, "basic", "erf", 256, m=1005)
+    _lib.set_operands(plan, 1000, 1024, 1024, 1000, 1000, 1024)
+    _lib.set_x_rows(plan, 5, 67, 335000, 1000, 5000)
+    assert (plan.x_d1, plan.x_d2, plan.x_s0, plan.x_s1, plan.x_s2) == (5, 67, 335000, 1000, 5000)
+    _lib.set_operands(plan, 1000, 1024, 1024, 1000, 1000, 1024)
+    assert (plan.x_d1, plan.x_d2) == (5, 67)
+    for bad in ((4, 67, 335000, 1000, 5000),       # d1*d2 does not divide m
+                (5, 67, 335000, 1000, 5004),       # stride not a multiple of 8
+                (5, 67, -8, 1000, 5000),           # negative stride
+                (5, 0, 335000, 1000, 5000),        # empty dim
+                (5, 67, 2 ** 29, 1000, 5000)):     # rows spread over 2^31 bytes
+        with pytest.raises(ValueError):
+            _lib.set_x_rows(plan, *bad)
+        assert (plan.x_d1, plan.x_d2, plan.x_s2) == (5, 67, 5000)
+    _lib.set_x_rows(plan, 0, 0, 0, 0, 0)
+    assert (plan.x_d1, plan.x_d2, plan.x_s0) == (0, 0, 0)
 
 
 def test_set_operands_validates_layout():
