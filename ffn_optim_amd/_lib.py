@@ -46,6 +46,7 @@ SIGNATURES = {
     "ffn_mi355x_query": (_i, [_i, _P(_i), ctypes.c_char_p, _i]),
     "ffn_mi355x_make_plan": (_i, [_i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _P(PlanStruct)]),
     "ffn_mi355x_workspace_bytes": (_i, [_P(PlanStruct), _P(ctypes.c_size_t)]),
+    "ffn_mi355x_workspace_counter_bytes": (_i, [_P(PlanStruct), _P(ctypes.c_size_t)]),
     "ffn_mi355x_set_operands": (_i, [_P(PlanStruct), _i, _i, _i, _i, _i, _i]),
     "ffn_mi355x_set_x_rows": (_i, [_P(PlanStruct), _i, _i, _i, _i, _i]),
     "ffn_mi355x_run": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
@@ -140,6 +141,13 @@ def make_plan(mp, kp, hp, np_, dtype, down_impl, gelu, block_num, up_variant=-1,
 def set_operands(plan: PlanStruct, k, h, n, ldx, ldw1, ldw2) -> None:
     """Point a native plan at operands of their logical widths (ffn_mi355x_set_operands)."""
     check(load().ffn_mi355x_set_operands(ctypes.byref(plan), k, h, n, ldx, ldw1, ldw2))
+
+
+def workspace_counter_bytes(plan: PlanStruct) -> int:
+    """Leading workspace bytes (arrival counters) that must be zero before first use."""
+    n = ctypes.c_size_t()
+    check(load().ffn_mi355x_workspace_counter_bytes(ctypes.byref(plan), ctypes.byref(n)))
+    return n.value
 
 
 def set_x_rows(plan: PlanStruct, d1, d2, s0, s1, s2) -> None:

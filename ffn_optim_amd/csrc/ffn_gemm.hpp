@@ -49,7 +49,9 @@ struct GemmParams {
     const void* a;        // [M][lda]   activations (X or hidden)
     const void* b;        // [N][ldb]   weights (W1 or W2)
     void* c;              // [M][ldc]   hidden or out
-    float* ws;            // Stream-K partial-tile slots (FP32)
+    float* ws;            // Stream-K partial-tile slots (FP32), ws_bytes long
+    unsigned* sk_flags;   // per split tile and wave: arrivals of the tile's pieces (zero between launches)
+    unsigned ws_bytes;
     int M, N, K;
     int m_valid;          // rows of A holding data; rows [m_valid, M) are zero padding
     int n_valid;          // rows of B holding data; rows [n_valid, N) read as zero
@@ -153,6 +155,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
     void* ptr = (void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
     // word3 0x00020000: raw (untyped) 32-bit data format, range-checked against `bytes`
     return __builtin_amdgcn_make_buffer_rsrc(ptr, (short)0, n, 0x00020000);
+}
+
+// Device-scope (SC1) 16-byte store and load of FP32 partials.  The eight XCDs have L2 caches of
+// their own: an SC1 store is written through to memory and an SC1 load reads past a stale L2
+// line, so a partial stored by one XCD and read by another after the arrival counter (below)
+// needs no cache writeback or invalidation.  These are the forms an agent-scope atomic store /
+// load takes on this target.
+constexpr int kCpolDevice = 16;  // SC1
+__device__ __forceinline__ void store_coherent(const __amdgpu_buffer_rsrc_t& r, uint32_t off, f32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, (int)off, 0, kCpolDevice);
+}
+__device__ __forceinline__ f32x4 load_coherent(const __amdgpu_buffer_rsrc_t& r, uint32_t off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kCpolDevice));
 }
 
 // s_waitcnt vmcnt(n) with lgkm/exp counters left alone (gfx9 encoding).
@@ -1045,8 +1060,10 @@ struct Engine {
     // a K-sliced tile first sums its slices (the exchange above) and each slice then writes the
     // row blocks [I0, I1) it owns.
     static constexpr int NTL = C::NT / C::WGK;
+    static __device__ __forceinline__ uint32_t part_off(int idx, int t) { return (uint32_t)(idx * NTL + t) * 16u; }
     template <int I0 = 0, int I1 = FM>
-    __device__ __forceinline__ void store_partial(float* slot, f32x16 (&acc)[FN][FM]) const {
+    __device__ __forceinline__ void store_partial(const __amdgpu_buffer_rsrc_t& r, uint32_t slot_off,
+                                                  f32x16 (&acc)[FN][FM]) const {
         const int t = tid - wk * NTL;
 #pragma unroll
         for (int j = 0; j < FN; ++j)
@@ -1057,29 +1074,122 @@ struct Engine {
                     const int idx = (j * FM + i) * 4 + q;
                     const f32x4 v = {acc[j][i][4 * q], acc[j][i][4 * q + 1], acc[j][i][4 * q + 2],
                                      acc[j][i][4 * q + 3]};
-                    *(f32x4*)(slot + ((size_t)idx * NTL + t) * 4) = v;
+                    store_coherent(r, slot_off + part_off(idx, t), v);
                     if (q == 3) __builtin_amdgcn_sched_barrier(0);
                 }
     }
-    template <int WK>
-    __device__ __forceinline__ void store_partial_sliced_as(float* slot, bool next, f32x16 (&acc)[FN][FM]) {
+
+    // Adds the partials of `c` pieces (slot byte offsets so[0..c), c <= PC, in K order) to the
+    // wave's positions, the first replacing them when `set`.  The loads of all c pieces (and,
+    // the blocks being unrolled, of several blocks) are in flight together; the sums are taken
+    // one piece after another.
+    template <int PC, int I0, int I1>
+    __device__ __forceinline__ void add_pieces(const __amdgpu_buffer_rsrc_t& r, const uint32_t (&so)[PC], int c,
+                                               bool set, int t, f32x16 (&acc)[FN][FM]) const {
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int i = I0; i < I1; ++i) {
+                f32x4 g[PC][4];
+#pragma unroll
+                for (int k = 0; k < PC; ++k)
+                    if (k < c)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) g[k][q] = load_coherent(r, so[k] + part_off((j * FM + i) * 4 + q, t));
+#pragma unroll
+                for (int k = 0; k < PC; ++k)
+                    if (k < c)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                acc[j][i][4 * q + e] = (set && k == 0) ? g[k][q][e] : acc[j][i][4 * q + e] + g[k][q][e];
+            }
+    }
+
+    // A Stream-K piece of split tile s, after its partial is stored: the wave counts itself in
+    // on the tile's counter for this wave (one counter per wave, since every wave stores and
+    // later reduces only the positions it holds), and the wave that arrives last -- its partial
+    // stores, like every other piece's, complete at device scope before its increment -- sums
+    // the pieces of its positions in ascending K order, resets the counter for the next launch,
+    // and stores its part of the tile through the register epilogue (bias, activation).  Nothing
+    // waits on another workgroup, so the grid needs no co-residency.  The sum is
+    // (...(p_first + p_first+1) + ...) + p_last, whichever piece arrives last: its own piece is
+    // used from registers when it is the first or one of two (a + b = b + a exactly), otherwise
+    // every piece is read back.
+    template <int EPI, int I0, int I1>
+    __device__ __forceinline__ void finish_piece(const GemmParams& p, const Unit& u, int v,
+                                                 const __amdgpu_buffer_rsrc_t& r, f32x16 (&acc)[FN][FM]) {
+        const int kI = p.k_iters, sp = u.split;
+        const int first = sk_owner(p, sp * kI), last = sk_owner(p, sp * kI + kI - 1);
+        wait_vmcnt<0>();
+        unsigned* flag = p.sk_flags + (size_t)sp * C::NW + wave;
+        unsigned old = 0;
+        if (lane == 0) old = __hip_atomic_fetch_add(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        old = (unsigned)__builtin_amdgcn_readfirstlane((int)old);
+        if (old != (unsigned)(last - first)) return;
+        if (lane == 0) __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int t = tid - wk * NTL;
+        auto slot_of = [&](int w) {
+            return (uint32_t)((sk_slot(p, w, sp - sk_start(p, w) / kI, C::BM * C::BN) - p.ws) * 4);
+        };
+        // own piece first or one of two: the others are added to it in K order; otherwise the
+        // sum starts over from the first piece and the own one is read back too.  Pieces are
+        // read PC at a time (several for a wave holding few blocks, whose registers allow it).
+        const bool keep = v == first || last - first == 1;
+        constexpr int PC = FN * (I1 - I0) <= 2 ? 4 : 1;
+        // k-th piece to add from w0 on (the own piece skipped when kept)
+        auto nth = [&](int w0, int k) { return w0 + k + ((keep && w0 <= v && w0 + k >= v) ? 1 : 0); };
+        bool set = !keep;
+        for (int w = first; nth(w, 0) <= last;) {
+            uint32_t so[PC];
+            int c = 0;
+#pragma unroll
+            for (int k = 0; k < PC; ++k) {
+                const int wk_ = nth(w, k);
+                so[k] = wk_ <= last ? slot_of(wk_) : 0u;
+                c += wk_ <= last ? 1 : 0;
+            }
+            add_pieces<PC, I0, I1>(r, so, c, set, t, acc);
+            set = false;
+            w = nth(w, PC - 1) + 1;
+        }
+        store_tile_regs<EPI, I0, I1>(p, u, acc);
+    }
+    template <int EPI, int WK>
+    __device__ __forceinline__ void finish_piece_sliced_as(const GemmParams& p, const Unit& u, int v,
+                                                           uint32_t slot_off, bool next, f32x16 (&acc)[FN][FM]) {
         if (next) wait_vmcnt<C::LOADS * (S - 1)>();
         else wait_vmcnt<0>();
         barrier();
         xphases<WK, 0>(acc);
-        store_partial<own_base(WK), own_base(WK) + own_rows(WK)>(slot, acc);
+        if constexpr (own_rows(WK) > 0) {
+            const __amdgpu_buffer_rsrc_t r = make_rsrc(p.ws, p.ws_bytes);
+            store_partial<own_base(WK), own_base(WK) + own_rows(WK)>(r, slot_off, acc);
+            finish_piece<EPI, own_base(WK), own_base(WK) + own_rows(WK)>(p, u, v, r, acc);
+        }
     }
-    // Partial of a Stream-K piece of a K-sliced tile: the slices are summed first (as for a whole
-    // tile), then each slice stores the blocks it owns.
-    __device__ __forceinline__ void store_partial_sliced(float* slot, bool next, f32x16 (&acc)[FN][FM]) {
-        if (wk == 0) store_partial_sliced_as<0>(slot, next, acc);
-        else store_partial_sliced_as<1>(slot, next, acc);
+    // A Stream-K piece: store its FP32 partial, then the last arrival finishes the tile.  A
+    // K-sliced tile sums its slices first (as for a whole tile) and each slice goes on with the
+    // blocks it owns.
+    template <int EPI>
+    __device__ __forceinline__ void finish_split(const GemmParams& p, const Unit& u, int v, bool next,
+                                                 f32x16 (&acc)[FN][FM]) {
+        const uint32_t slot_off = (uint32_t)((sk_slot(p, v, u.local, C::BM * C::BN) - p.ws) * 4);
+        if constexpr (C::WGK > 1) {
+            if (wk == 0) finish_piece_sliced_as<EPI, 0>(p, u, v, slot_off, next, acc);
+            else finish_piece_sliced_as<EPI, 1>(p, u, v, slot_off, next, acc);
+        } else {
+            const __amdgpu_buffer_rsrc_t r = make_rsrc(p.ws, p.ws_bytes);
+            store_partial(r, slot_off, acc);
+            finish_piece<EPI, 0, FM>(p, u, v, r, acc);
+        }
     }
 };
 
 // Persistent GEMM: every workgroup walks its units (whole tiles, then for Stream-K its split
 // iterations) with the DMA of the next unit overlapping the epilogue of the current one.
-// Split pieces that share a tile publish FP32 partials; ffn_sk_reduce_kernel finishes them.
+// Split pieces that share a tile publish FP32 partials; the last to arrive finishes the tile.
 template <int DT, class C, int EPI, bool SK, bool FASTK, bool GATHER = false>
 __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
     // The activation epilogue stores from registers, where its VALU work overlaps the stores;
@@ -1119,11 +1229,9 @@ __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
     while (true) {
         const Unit nx = walk.next(p);
         eng.template mainloop<FASTK>(p, u, nx, acc);
-        if (SK && u.split >= 0) {
-            float* slot = sk_slot(p, v, u.local, C::BM * C::BN);
-            if constexpr (C::WGK > 1) eng.store_partial_sliced(slot, nx.valid, acc);
-            else eng.store_partial(slot, acc);
-        } else if constexpr (C::WGK > 1)
+        if (SK && u.split >= 0)
+            eng.template finish_split<EPI>(p, u, v, nx.valid, acc);
+        else if constexpr (C::WGK > 1)
             eng.template store_sliced<EPI>(p, u, nx.valid, acc);
         else if constexpr (EPI_IN_REGS)
             eng.template store_tile_regs<EPI>(p, u, acc);
@@ -1131,62 +1239,6 @@ __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
             eng.template store_tile_lds<EPI>(p, u, nx.valid, acc);
         if (!nx.valid) break;
         u = nx;
-    }
-}
-
-// Stream-K fixup, stream-ordered after ffn_gemm_kernel<..., true>: workgroup (s, b) sums the
-// FP32 partials of 32x32 accumulator block b (of every wave) of split tile s in ascending K
-// order (independent of which workgroup finished first), applies the epilogue's activation
-// (none for the down GEMM, the GELU for a split up GEMM), rounds once to the storage type and
-// stores.  Each thread keeps the four 16-byte groups of its block in flight per piece, and the
-// same lane pairing as the GEMM's register epilogue (v_permlane32_swap) turns its output into
-// two 16-byte row segments.
-template <int DT, class C, int EPI>
-__global__ void __launch_bounds__(C::NT) ffn_sk_reduce_kernel(GemmParams p, int blocks) {
-    static_assert(EPI != EPI_SWIGLU, "a SwiGLU up GEMM is never split: its block pairs leave together");
-    constexpr int TE = C::BM * C::BN;
-    const int s = blockIdx.x / blocks, ji = blockIdx.x - s * blocks;
-    const int kI = p.k_iters;
-    const int first = sk_owner(p, s * kI), last = sk_owner(p, s * kI + kI - 1);
-    if (first == last) return;  // stored whole by its only contributor
-    int tm, tn;
-    tile_coords(p, p.dp_tiles + s, tm, tn);
-    // launched with the threads of one K slice (NTL = NT / WGK): thread t is the partial
-    // layout's logical thread (Engine::store_partial)
-    constexpr int NTL = C::NT / C::WGK;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave % C::WGM, wn = wave / C::WGM;
-    const int j = ji / C::FM, i = ji - j * C::FM;
-    f32x4 tot[4];
-    {
-        const float* slot = sk_slot(p, first, s - sk_start(p, first) / kI, TE);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) tot[q] = *(const f32x4*)(slot + ((size_t)(ji * 4 + q) * NTL + tid) * 4);
-    }
-    for (int w = first + 1; w <= last; ++w) {
-        const float* slot = sk_slot(p, w, s - sk_start(p, w) / kI, TE);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) tot[q] += *(const f32x4*)(slot + ((size_t)(ji * 4 + q) * NTL + tid) * 4);
-    }
-    const int bcol = tn * C::BN + wn * C::WTN + 32 * j + 4 * (lane >> 5);
-    if (p.bias) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) tot[q] += bias4<DT>(p, bcol + 8 * q);
-    }
-    u32x2 g[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-        g[q] = pack4<DT>(activate<EPI>(tot[q].x), activate<EPI>(tot[q].y), activate<EPI>(tot[q].z),
-                         activate<EPI>(tot[q].w));
-    const int m = tm * C::BM + wm * C::WTM + 32 * i + (lane & 31);
-    const int n0 = tn * C::BN + wn * C::WTN + 32 * j + 8 * (lane >> 5);
-#pragma unroll
-    for (int pp = 0; pp < 2; ++pp) {
-        const auto s0 = __builtin_amdgcn_permlane32_swap(g[2 * pp].x, g[2 * pp + 1].x, false, false);
-        const auto s1 = __builtin_amdgcn_permlane32_swap(g[2 * pp].y, g[2 * pp + 1].y, false, false);
-        const u32x4 v = {(uint32_t)s0[0], (uint32_t)s1[0], (uint32_t)s0[1], (uint32_t)s1[1]};
-        const int n = n0 + 16 * pp;
-        if (m < p.M && n < p.c_cols) *(u32x4*)((char*)p.c + ((size_t)m * (size_t)p.ldc + (size_t)n) * 2) = v;
     }
 }
 

@@ -30,8 +30,8 @@ namespace {
 // one launch of ffn_gemm_kernel with the DMA addressing the plan chose
 template <class CFG, int EPI, bool SK>
 void launch_gemm(const ffn::GemmParams* p, dim3 g, dim3 b, hipStream_t stream) {
-    if constexpr (EPI != ffn::EPI_STORE || SK) {
-        // up roles (and the split GEMM, which a split up uses) may read gathered activation rows
+    if constexpr (EPI != ffn::EPI_STORE) {
+        // up roles may read gathered activation rows
         if (p->a_gather) {
             hipLaunchKernelGGL((ffn::ffn_gemm_kernel<FFN_DT, CFG, EPI, SK, false, true>), g, b, 0, stream, *p);
             return;
@@ -43,37 +43,10 @@ void launch_gemm(const ffn::GemmParams* p, dim3 g, dim3 b, hipStream_t stream) {
         hipLaunchKernelGGL((ffn::ffn_gemm_kernel<FFN_DT, CFG, EPI, SK, false>), g, b, 0, stream, *p);
 }
 
-// Stream-K GEMM writing FP32 partials, then the fixup that sums every split tile, applies the
-// activation EPI and stores it (K-sliced tiles included: their slices are summed before a
-// partial is written).  Whole tiles of the GEMM leave through the plain cast, so a
-// split up GEMM (EPI a GELU) must have none.
-template <class CFG, int EPI>
-hipError_t launch_split(const ffn::GemmParams* p, dim3 g, dim3 b, hipStream_t stream) {
-    using namespace ffn;
-    if constexpr (EPI != EPI_STORE) {
-        // an activation is applied by the fixup only: every tile must be split and shared
-        if (p->dp_tiles != 0) return hipErrorInvalidValue;
-        const int kI = p->k_iters;
-        for (int s = 0; s < p->sk_tiles; ++s)
-            if (sk_owner(*p, s * kI) == sk_owner(*p, s * kI + kI - 1)) return hipErrorInvalidValue;
-    }
-    launch_gemm<CFG, EPI_STORE, true>(p, g, b, stream);
-    if (p->sk_tiles > 0) {
-        // one reduce workgroup per 32x32 accumulator block of each split tile: every partial
-        // load of the fixup is then in flight at once (a workgroup walking several blocks
-        // serialises their memory latencies); the threads of one K slice cover the tile
-        constexpr int blocks = CFG::FN * CFG::FM;
-        hipLaunchKernelGGL((ffn_sk_reduce_kernel<FFN_DT, CFG, EPI>), dim3(p->sk_tiles * blocks),
-                           dim3(CFG::NT / CFG::WGK), 0, stream, *p, blocks);
-    }
-    return hipSuccess;
-}
-
 template <class CFG>
 hipError_t launch_role(int role, const ffn::GemmParams* p, int grid, hipStream_t stream) {
     using namespace ffn;
     const dim3 g(grid), b(CFG::NT);
-    hipError_t e = hipSuccess;
     switch (role) {
         case FFN_ROLE_UP_ERF:
             launch_gemm<CFG, EPI_GELU_ERF, false>(p, g, b, stream);
@@ -85,13 +58,13 @@ hipError_t launch_role(int role, const ffn::GemmParams* p, int grid, hipStream_t
             launch_gemm<CFG, EPI_STORE, false>(p, g, b, stream);
             break;
         case FFN_ROLE_DOWN_STREAMK:
-            e = launch_split<CFG, EPI_STORE>(p, g, b, stream);
+            launch_gemm<CFG, EPI_STORE, true>(p, g, b, stream);
             break;
         case FFN_ROLE_UP_SPLIT_ERF:
-            e = launch_split<CFG, EPI_GELU_ERF>(p, g, b, stream);
+            launch_gemm<CFG, EPI_GELU_ERF, true>(p, g, b, stream);
             break;
         case FFN_ROLE_UP_SPLIT_RATIONAL:
-            e = launch_split<CFG, EPI_GELU_RATIONAL>(p, g, b, stream);
+            launch_gemm<CFG, EPI_GELU_RATIONAL, true>(p, g, b, stream);
             break;
         case FFN_ROLE_UP_SILU:
             launch_gemm<CFG, EPI_SILU, false>(p, g, b, stream);
@@ -101,12 +74,11 @@ hipError_t launch_role(int role, const ffn::GemmParams* p, int grid, hipStream_t
             else return hipErrorInvalidValue;
             break;
         case FFN_ROLE_UP_SPLIT_SILU:
-            e = launch_split<CFG, EPI_SILU>(p, g, b, stream);
+            launch_gemm<CFG, EPI_SILU, true>(p, g, b, stream);
             break;
         default:
             return hipErrorInvalidValue;
     }
-    if (e != hipSuccess) return e;
     return hipGetLastError();
 }
 }  // namespace

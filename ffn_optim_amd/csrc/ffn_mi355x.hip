@@ -86,8 +86,8 @@ constexpr double kCuMfmaRate = 4.8e12;     // FLOP/s per CU a 256x256 tile susta
 constexpr double kCuLoadRate = 60e9;       // B/s per CU of LDS-DMA alongside MFMA work
 constexpr double kLoadLatency = 0.8e-6;    // s, L2/MALL load latency under load
 constexpr double kHbmRate = 6.5e12;        // B/s sustained HBM read rate
-constexpr double kLaunch = 3e-6;           // s, one extra kernel launch (Stream-K fixup)
-constexpr double kReduceRate = 3.0e12;     // B/s of the fixup kernel
+constexpr double kFinishLatency = 1.2e-6;  // s, one dependent step of a split tile's finish:
+                                           // partial write-through, arrival count, partial reads
 constexpr double kUnitOverhead = 2.5e-6;   // s per unit: DMA prologue latency + epilogue
 
 // Relative MFMA efficiency of each macro tile (measured on the FFN shapes, 256x256 = 1): the
@@ -133,25 +133,29 @@ struct SkShape {
 };
 
 // Stream-K grid: block_num workgroups, or fewer when every tile is split (fewer tiles than
-// workgroups) and a piece count p that divides the tile's iterations gives T*p >= 90% of them:
-// each workgroup then covers exactly one piece of one tile, none straddles two tiles and needs
-// a second partial slot.  On the 16x5120 -> 13824 -> 5120 decode down, 240 workgroups (80 tiles
-// x 3 pieces of 72 iterations) measured 6% faster than 256 with pieces of 67.5.
+// workgroups): p pieces per tile, p a divisor of the tile's iterations where one exists (each
+// workgroup then covers exactly one piece of one tile, none straddles two tiles and needs a
+// second partial slot), p at most kMaxPieces: the last piece of a tile reads the others' partials
+// in a chain of dependent loads that grows with p.  On the 16x5120 -> 13824 -> 5120 decode down,
+// 240 workgroups (80 tiles x 3 pieces of 72 iterations) measured 6% faster than 256 with pieces
+// of 67.5; on the smallest FFN's down (8 tiles), 16 one-iteration pieces per tile measured 24%
+// slower than a separate reduction launch.
+constexpr long long kMaxPieces = 4;
 long long sk_grid(long long tiles, long long k_iters, int G) {
-    if (tiles >= G) return G;
-    // no more workgroups than split iterations: every workgroup then has work, and the
-    // workspace holds no slots for idle ones
-    if (tiles * k_iters <= G) return tiles * k_iters;
-    for (long long p = G / tiles; p >= 2; --p) {
-        if (k_iters % p) continue;
-        if (tiles * p * 10 >= (long long)G * 9) return tiles * p;
-        break;
-    }
-    return G;
+    const long long pmax = std::min<long long>({(long long)G / std::max<long long>(1, tiles), kMaxPieces, k_iters});
+    if (tiles >= G || pmax < 2) return G;
+    for (long long p = pmax; p >= 2; --p)
+        if (k_iters % p == 0) return tiles * p;
+    return tiles * pmax;
 }
 
 // Tiles of a GEMM whose rows [m_valid, M) are zero padding: only tile rows holding data are
 // computed (the kernel zero-fills the rows past them).
+// Arrival counters of split tiles (one per tile and wave) live in a fixed region at the start
+// of the workspace; a split schedule needing more than it holds is not used.
+constexpr size_t kCounterBytes = FFN_MI355X_WORKSPACE_COUNTER_BYTES;
+bool counters_fit(long long split_tiles, const Variant& v) { return split_tiles * v.nw * 4 <= (long long)kCounterBytes; }
+
 bool sk_shape(const Variant& v, long long m_valid, long long N, long long K, int block_num, SkShape& s) {
     s.tiles = cdiv(m_valid, v.bm) * cdiv(N, v.bn);
     s.k_iters = cdiv(K, v.bk);
@@ -165,7 +169,7 @@ bool sk_shape(const Variant& v, long long m_valid, long long N, long long K, int
     const long long span = s.q + (s.r ? 1 : 0);
     // a range of `span` iterations touches at most ceil(span / k_iters) + 1 tiles
     s.slots = cdiv(span, s.k_iters) + 1;
-    return s.sk > 0 && s.k_iters >= 2;
+    return s.sk > 0 && s.k_iters >= 2 && counters_fit(s.sk, v);
 }
 
 double cost_streamk(const Variant& v, const SkShape& s, long long m_valid, long long N, long long K) {
@@ -175,12 +179,15 @@ double cost_streamk(const Variant& v, const SkShape& s, long long m_valid, long 
     const long long sk_iters = s.q + (s.r ? 1 : 0);
     double t = it * ((double)dp_waves * s.k_iters + (double)sk_iters) +
                kUnitOverhead * (double)(dp_waves + 1);
-    // shared split tiles: FP32 partials written, re-read and reduced by a second launch
+    // shared split tiles: each piece writes its FP32 partial through to memory and counts in;
+    // the last reads the others (several at a time when its waves hold at most two 32x32
+    // blocks, one at a time otherwise) and stores the tile
     const long long pieces_per_tile = std::min<long long>(G, cdiv(s.k_iters, std::max<long long>(1, s.q)) + 1);
     if (s.k_iters > sk_iters) {
         const double tile_bytes = (double)v.bm * v.bn * 4.0;
-        t += kLaunch + (double)s.sk * (double)pieces_per_tile * 2.0 * tile_bytes / kReduceRate +
-             tile_bytes / kCuLoadRate;
+        const long long per_read = (long long)v.bm * v.bn / v.nw <= 2048 ? 4 : 1;
+        t += kFinishLatency * (double)(2 + cdiv(pieces_per_tile - 1, per_read)) +
+             (double)pieces_per_tile * tile_bytes / kCuLoadRate;
     }
     const double hbm = (double)(N * K + m_valid * K) * 2.0 / kHbmRate;
     return std::max(t, hbm);
@@ -210,23 +217,15 @@ int pick_streamk(long long M, long long m_valid, long long N, long long K, int G
 
 // Split up GEMM: taken when the up's tiles would leave at least half of the workgroups idle and
 // the reduction is deep enough to split (a decode-size FFN with a narrow H, e.g. one GPU's H/8
-// share of a 16x5120 -> 13824 FFN: 27 tiles that stream W1 on 27 CUs).  Every tile must then
-// be split and shared by two or more workgroups: the GEMM stores its partials only, and the
-// fixup applies the GELU.  (A whole tile would leave the Stream-K GEMM through the plain cast.)
-// The grid cuts every tile into the largest number of equal pieces p <= G / tiles that divides
-// its iterations (none straddles two tiles), else uses all G: on that decode shard, 216
-// workgroups (8 pieces of 10 iterations) measured 12.6 us and 108 (4 of 20) 12.2 us, against
-// 14.0 us for 256 uneven pieces and 19.9 us unsplit.
+// share of a 16x5120 -> 13824 FFN, whose few tiles would stream W1 on a few CUs).  Every tile is
+// then cut into p equal pieces (sk_grid); the last piece of a tile to finish sums the partials
+// and applies the activation.  On that decode shard (54 tiles of 32x32, 4 pieces of 10
+// iterations on 216 workgroups) the split up takes 10.6-10.8 us.
 constexpr int kUpSplitMinIters = 16;
 bool split_up(const Variant& v, long long m_valid, long long N, long long K, int G, SkShape& s) {
     const long long tiles = cdiv(m_valid, v.bm) * cdiv(N, v.bn), k_iters = cdiv(K, v.bk);
     if (tiles * 2 > G || k_iters < kUpSplitMinIters) return false;
-    long long grid = G;
-    for (long long p = G / tiles; p >= 2; --p)
-        if (k_iters % p == 0) {
-            grid = tiles * p;
-            break;
-        }
+    const long long grid = sk_grid(tiles, k_iters, G);
     if (!sk_shape(v, m_valid, N, K, (int)grid, s) || s.grid != grid || s.dp != 0 || s.sk != tiles) return false;
     const long long kI = s.k_iters, big = (s.q + 1) * s.r;
     auto owner = [&](long long x) { return s.q == 0 ? x : x < big ? x / (s.q + 1) : s.r + (x - big) / s.q; };
@@ -364,6 +363,13 @@ bool valid_plan(const ffn_mi355x_plan* p) {
            p->activation >= FFN_MI355X_GELU_ERF && p->activation <= FFN_MI355X_SWIGLU && p->block_num >= 1;
 }
 
+// Workspace layout: a fixed region of arrival counters first (one per split tile and wave, for
+// the split up GEMM and the Stream-K down alike, which run one after the other; every launch
+// leaves them zero), then the FP32 partial-tile slots.  The region has the same size for every
+// plan, so one zero-filled workspace serves any plans in turn: no plan's slots overlap another
+// plan's counters.
+size_t flags_bytes(const ffn_mi355x_plan*) { return kCounterBytes; }
+
 int launch(const Variant& v, int dtype, int role, const ffn::GemmParams& gp, int grid,
            void* stream) {
     const hipError_t e = v.launch[dtype](role, &gp, grid, (hipStream_t)stream);
@@ -455,6 +461,10 @@ int ffn_mi355x_make_plan(int m, int mp, int kp, int hp, int np, int dtype, int d
                 if (s.k_iters < 2)
                     return fail(FFN_MI355X_ENOT_APPLICABLE,
                                 "Stream-K candidate requires at least two K tiles along H");
+                if (s.sk > 0)
+                    return fail(FFN_MI355X_ENOT_APPLICABLE,
+                                "Stream-K candidate splits more tiles (%lld) than the workspace counters "
+                                "hold for this block_num", s.sk);
                 return fail(FFN_MI355X_ENOT_APPLICABLE,
                             "Stream-K candidate has no remainder tiles for this block_num");
             }
@@ -493,6 +503,10 @@ int ffn_mi355x_make_plan(int m, int mp, int kp, int hp, int np, int dtype, int d
         plan->workspace_bytes = 0;
     }
     if (up_ws > plan->workspace_bytes) plan->workspace_bytes = up_ws;
+    if (plan->workspace_bytes > 0) plan->workspace_bytes += flags_bytes(plan);
+    // the kernels address partial slots with 32-bit buffer offsets
+    if (plan->workspace_bytes >= (size_t)1 << 31)
+        return fail(FFN_MI355X_EINVAL, "workspace of %zu bytes exceeds 2 GiB", plan->workspace_bytes);
     plan->k = kp, plan->h = hp, plan->n = np;
     plan->ldx = kp, plan->ldw1 = kp, plan->ldw2 = hp;
     plan->x_d1 = plan->x_d2 = plan->x_s0 = plan->x_s1 = plan->x_s2 = 0;
@@ -540,9 +554,23 @@ int ffn_mi355x_workspace_bytes(const ffn_mi355x_plan* plan, size_t* bytes) {
     return ok();
 }
 
+int ffn_mi355x_workspace_counter_bytes(const ffn_mi355x_plan* plan, size_t* bytes) {
+    if (!plan || !bytes) return fail(FFN_MI355X_EINVAL, "NULL argument");
+    if (!valid_plan(plan)) return fail(FFN_MI355X_EINVAL, "invalid plan");
+    *bytes = plan->workspace_bytes > 0 ? flags_bytes(plan) : 0;
+    return ok();
+}
+
 }  // extern "C"
 
 namespace {
+
+void set_workspace(ffn::GemmParams& gp, const ffn_mi355x_plan* plan, void* ws) {
+    const size_t f = flags_bytes(plan);
+    gp.sk_flags = (unsigned*)ws;
+    gp.ws = (float*)((char*)ws + f);
+    gp.ws_bytes = (unsigned)(plan->workspace_bytes - f);
+}
 
 // Up GEMM of a plan.  ws_scratch: ws is this library's scratch array (its size is known, and it
 // is not a HIP allocation of its own to look up).
@@ -600,7 +628,7 @@ int run_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, const voi
         gp.sk_q = (int)(total / plan->up_grid);
         gp.sk_r = (int)(total % plan->up_grid);
         gp.slots_per_wg = plan->up_slots_per_wg;
-        gp.ws = (float*)ws;
+        set_workspace(gp, plan, ws);
         const int role = plan->activation == FFN_MI355X_GELU_ERF        ? FFN_ROLE_UP_SPLIT_ERF
                          : plan->activation == FFN_MI355X_GELU_RATIONAL ? FFN_ROLE_UP_SPLIT_RATIONAL
                                                                         : FFN_ROLE_UP_SPLIT_SILU;
@@ -655,7 +683,7 @@ int run_down(const ffn_mi355x_plan* plan, const void* hidden, const void* w2, co
         gp.sk_q = (int)(total / G);
         gp.sk_r = (int)(total % G);
         gp.slots_per_wg = plan->down_slots_per_wg;
-        gp.ws = (float*)ws;
+        set_workspace(gp, plan, ws);
         return launch(D, plan->dtype, FFN_ROLE_DOWN_STREAMK, gp, G, hip_stream);
     }
     gp.dp_tiles = plan->down_tiles;

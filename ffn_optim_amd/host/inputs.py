@@ -186,8 +186,9 @@ def interleave_gate_up(weight, h, hp):
 def prepare_storage(x, weight1, weight2, plan, alias_aligned=False, bias1=None, bias2=None):
     """Contiguise and zero-pad into [mp,kp], [hp,kp], [np,hp]; allocate hidden, out, workspace.
 
-    Same buffers as ops/host/inputs.py:74-90; the FP32 workspace holds the partial tiles of
-    the Stream-K down and of a split up GEMM (every slot is written before it is read).
+    Same buffers as ops/host/inputs.py:74-90; the FP32 workspace holds the arrival counters and
+    partial tiles of the Stream-K down and of a split up GEMM (allocated zero-filled; every
+    partial slot is written before it is read).
     Returns the six buffers, the operand layout (k, h, n, ldx, ldw1, ldw2) for
     ffn_mi355x_set_operands and X's row grid (d1, d2, s0, s1, s2) for ffn_mi355x_set_x_rows,
     or None when X is read as rows at pitch ldx.
@@ -204,7 +205,9 @@ def prepare_storage(x, weight1, weight2, plan, alias_aligned=False, bias1=None, 
     p = plan.problem
     hidden = torch.empty((plan.mp, plan.hp), device=x.device, dtype=x.dtype)
     out = torch.empty((plan.mp, plan.np), device=x.device, dtype=x.dtype)
-    ws = torch.empty(plan.workspace_shape, device=x.device, dtype=torch.float32)
+    # zero-filled: its leading bytes are the split tiles' arrival counters, which every launch
+    # leaves zero again
+    ws = torch.zeros(plan.workspace_shape, device=x.device, dtype=torch.float32)
     grid = row_grid(x, p.k) if alias_aligned else None
     x_rows = None
     if grid is not None and grid[0] == "pitch":

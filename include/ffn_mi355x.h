@@ -132,18 +132,30 @@ int ffn_mi355x_set_operands(ffn_mi355x_plan* plan, int k, int h, int n, int ldx,
  * on a bad grid, plan unchanged. */
 int ffn_mi355x_set_x_rows(ffn_mi355x_plan* plan, int d1, int d2, int s0, int s1, int s2);
 
-/* Workspace bytes a plan needs (0 for the Basic down). */
+/* Workspace bytes a plan needs (0 for the Basic down without a split up GEMM). */
 int ffn_mi355x_workspace_bytes(const ffn_mi355x_plan* plan, size_t* bytes);
+
+/* Bytes at the start of every workspace that hold the split tiles' arrival counters (one
+ * 32-bit counter per split tile and wave).  They must be zero before a workspace's first use
+ * (e.g. allocate it zero-filled); every call leaves them zero again, so a workspace can serve
+ * any plans whose workspace_bytes it covers, one call after another.  The rest of the
+ * workspace needs no initialisation.  No counterpart in the reference, whose Stream-K reduction
+ * is a separate phase (ops/kernel/ffn.py:1035-1175). */
+#define FFN_MI355X_WORKSPACE_COUNTER_BYTES (64u << 10)
+
+/* FFN_MI355X_WORKSPACE_COUNTER_BYTES when the plan needs a workspace, else 0. */
+int ffn_mi355x_workspace_counter_bytes(const ffn_mi355x_plan* plan, size_t* bytes);
 
 /* The whole FFN: up GEMM + GELU epilogue writing `hidden` [mp,hp] in the input
  * dtype, then the Basic or Stream-K down GEMM writing `out` [mp,np].  Replaces
  * the single artifact(*tensors, block_num) launch of ops/api.py:43 built by
  * compile_kernel (ops/host/dispatch.py:97-116) from ops/kernel/ffn.py.
  * `ws` must hold plan->workspace_bytes whenever that is nonzero (Stream-K down or
- * split up); it may be NULL otherwise.
- * The Stream-K down is two launches: the split GEMM writing FP32 partial tiles
- * to `ws`, then the fixup summing them in ascending K order and rounding once.
- * A split up is the same two launches with the GELU applied in the fixup. */
+ * split up), its counter bytes zero (ffn_mi355x_workspace_counter_bytes); it may be NULL
+ * otherwise.
+ * The Stream-K down is one launch: the pieces of a split tile store FP32 partial tiles to `ws`,
+ * and the last piece to arrive sums them in ascending K order, rounds once and stores the tile.
+ * A split up is the same with the GELU applied after the sum. */
 int ffn_mi355x_run(const ffn_mi355x_plan* plan, const void* x, const void* w1,
                    const void* w2, void* hidden, void* out, void* ws, void* hip_stream);
 
@@ -158,7 +170,8 @@ int ffn_mi355x_run(const ffn_mi355x_plan* plan, const void* x, const void* w1,
  * the scratch is refused with FFN_MI355X_EINVAL before any launch.  The call allocates and
  * frees nothing.  Every call on one GPU shares that GPU's scratch: calls that overlap on one GPU
  * (on different streams, or from different threads) race and must be serialised by the caller.
- * Every partial is written before it is read within a call, so nothing needs clearing. */
+ * The scratch starts zero-filled and every call leaves its arrival counters zero again; every
+ * partial is written before it is read within a call, so nothing needs clearing. */
 int ffn_mi355x_run_noalloc(const ffn_mi355x_plan* plan, const void* x, const void* w1,
                            const void* w2, void* hidden, void* out, void* hip_stream);
 
@@ -180,7 +193,8 @@ int ffn_mi355x_down_ex(const ffn_mi355x_plan* plan, const void* hidden, const vo
 
 /* Stage 1 alone: up-projection with GELU epilogue (ops/kernel/ffn.py:207-360,
  * 540-581, the cube/vector up regions of both kernels).  `ws` holds
- * plan->workspace_bytes when plan->up_sk_tiles > 0 (split up); it may be NULL otherwise. */
+ * plan->workspace_bytes, counters zero, when plan->up_sk_tiles > 0 (split up); it may be NULL
+ * otherwise. */
 int ffn_mi355x_up(const ffn_mi355x_plan* plan, const void* x, const void* w1,
                   void* hidden, void* ws, void* hip_stream);
 

@@ -13,6 +13,7 @@ import torch
 from ffn_optim_amd import _lib, eagle_ffn_linear, prepare_eagle_ffn
 from ffn_optim_amd.host.inputs import interleave_gate_up
 from oracle.reference import compare, ffn_torch
+from gpu_workspace import counters_are_zero, poisoned_workspace
 
 pytestmark = pytest.mark.gpu
 
@@ -129,10 +130,11 @@ def test_up_integer_activation_all_variants(dtype, activation):
             assert activation == "swiglu"   # a tile without whole 64-column block pairs
             continue
         hidden = torch.full((mp, hp), float("nan"), dtype=dtype, device="cuda")
-        ws = torch.full((max(1, plan.workspace_bytes // 4),), float("nan"), dtype=torch.float32, device="cuda")
+        ws = poisoned_workspace(plan)
         _lib.check(lib.ffn_mi355x_up_ex(ctypes.byref(plan), xd.data_ptr(), w1d.data_ptr(), b1d.data_ptr(),
                                         hidden.data_ptr(), ws.data_ptr(), stream))
         torch.cuda.synchronize()
+        assert counters_are_zero(plan, ws), (activation, variant)
         ulps = (_ordinal(hidden.cpu().view(torch.int16)) - _ordinal(truth.view(torch.int16))).abs()
         say("up-act", activation, dtype, variant, plan.up_sk_tiles, int(ulps.max()), int((ulps > 0).sum()))
         assert int(ulps.max()) <= 1, (activation, variant)
@@ -162,9 +164,10 @@ def test_down_integer_bias_bit_exact(dtype):
             except ValueError:
                 continue
             out = torch.full((mp, np_), float("nan"), dtype=dtype, device="cuda")
-            ws = torch.full((max(1, plan.workspace_bytes // 4),), float("nan"), dtype=torch.float32, device="cuda")
+            ws = poisoned_workspace(plan)
             _lib.check(lib.ffn_mi355x_down_ex(ctypes.byref(plan), hid_d.data_ptr(), w2_d.data_ptr(),
                                               b2_d.data_ptr(), out.data_ptr(), ws.data_ptr(), stream))
             torch.cuda.synchronize()
+            assert counters_are_zero(plan, ws), (variant, down, block_num)
             say("down-bias", dtype, variant, down, block_num)
             assert torch.equal(out.cpu().view(torch.int16), golden.view(torch.int16)), (variant, down, block_num)

@@ -13,6 +13,7 @@ import torch
 from ffn_optim_amd import _lib, prepare_ffn
 from ffn_optim_amd.cases import V1_CASES, get_case, load_cases, make_inputs
 from oracle.reference import compare, ffn_rows, ffn_torch, gelu_erf, gelu_rational
+from gpu_workspace import counters_are_zero, poisoned_workspace
 
 pytestmark = pytest.mark.gpu
 
@@ -278,13 +279,13 @@ def test_down_integer_bit_exact_all_variants(dtype, hp):
                 continue
             say("down-exact", dtype, variant, down, block_num, plan.to_dict())
             out = torch.full((mp, np_), float("nan"), dtype=dtype, device="cuda")
-            ws = torch.full((max(1, plan.workspace_bytes // 4),), float("nan"), dtype=torch.float32,
-                            device="cuda")
+            ws = poisoned_workspace(plan)
             _lib.check(lib.ffn_mi355x_down(ctypes.byref(plan), hid_d.data_ptr(), w2_d.data_ptr(),
                                            out.data_ptr(), ws.data_ptr(), stream))
             torch.cuda.synchronize()
             assert torch.equal(out.cpu().view(torch.int16), golden.view(torch.int16)), \
                 (variant, down, block_num)
+            assert counters_are_zero(plan, ws), (variant, down, block_num)
 
 
 def _ordinal(bits16):
@@ -314,11 +315,11 @@ def test_up_integer_gelu_all_variants(dtype, kp):
             plan = _lib.make_plan(mp, kp, hp, 64, _lib.BF16 if dtype == torch.bfloat16 else _lib.FP16,
                                   "basic", gelu, 256, variant, -1)
             hidden = torch.full((mp, hp), float("nan"), dtype=dtype, device="cuda")
-            ws = torch.full((max(1, plan.workspace_bytes // 4),), float("nan"), dtype=torch.float32,
-                            device="cuda")
+            ws = poisoned_workspace(plan)
             _lib.check(lib.ffn_mi355x_up(ctypes.byref(plan), xd.data_ptr(), w1d.data_ptr(),
                                          hidden.data_ptr(), ws.data_ptr(), stream))
             torch.cuda.synchronize()
+            assert counters_are_zero(plan, ws), (gelu, variant)
             got = hidden.cpu()
             if gelu == "erf":
                 ulps = (_ordinal(got.view(torch.int16)) - _ordinal(truth_erf.view(torch.int16))).abs()
@@ -492,3 +493,52 @@ def test_gathered_x_every_variant(dtype):
             torch.cuda.synchronize()
             assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), v
         assert_parity(y, x, w1, w2, tag=f"gathered X {dtype} {(d1, d0, k)}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_streamk_finish_reproducible_and_resets(dtype):
+    """The Stream-K pieces of a tile are summed by whichever arrives last, in ascending K order:
+    random (non-integer) operands give bit-identical outputs over repeated launches whatever the
+    arrival order, for tiles of two and of three or more pieces and K-sliced tiles.  One
+    zero-filled workspace serves all the plans in turn (each launch leaves its counters zero),
+    and every output passes the criterion against the golden."""
+    lib = _lib.load()
+    gen = torch.Generator().manual_seed(17)
+    mp, hp, np_ = 320, 2048, 448
+    hid = torch.randn(mp, hp, generator=gen).to(dtype)
+    w2 = (torch.randn(np_, hp, generator=gen) * hp ** -0.5).to(dtype)
+    golden = (hid.double() @ w2.double().T).float().to(dtype)
+    hid_d, w2_d = hid.cuda(), w2.cuda()
+    stream = torch.cuda.current_stream().cuda_stream
+    plans = []
+    for variant in range(lib.ffn_mi355x_num_variants()):
+        for block_num in (256, 37, 5):
+            try:
+                plans.append((variant, block_num, _plan(mp, 64, hp, np_, dtype, "streamk", block_num, 0, variant)))
+            except ValueError:
+                pass
+    assert len(plans) >= 20
+    ws = torch.zeros(max(p.workspace_bytes for _, _, p in plans) // 4 + 1, dtype=torch.float32, device="cuda")
+    def owner(x, q, r):      # workgroup of split iteration x (q iterations each, one more for the first r)
+        return x if q == 0 else (x // (q + 1) if x < (q + 1) * r else r + (x - (q + 1) * r) // q)
+
+    pieces_seen = set()
+    for variant, block_num, plan in plans:
+        kI, total = plan.down_k_iters, plan.down_sk_tiles * plan.down_k_iters
+        q, r = total // plan.down_grid, total % plan.down_grid
+        pieces_seen.add(max(owner(s * kI + kI - 1, q, r) - owner(s * kI, q, r) + 1
+                            for s in range(plan.down_sk_tiles)))
+        outs = []
+        for _ in range(4):
+            out = torch.full((mp, np_), float("nan"), dtype=dtype, device="cuda")
+            _lib.check(lib.ffn_mi355x_down(ctypes.byref(plan), hid_d.data_ptr(), w2_d.data_ptr(),
+                                           out.data_ptr(), ws.data_ptr(), stream))
+            outs.append(out)
+        torch.cuda.synchronize()
+        say("sk-repro", dtype, variant, block_num, plan.down_sk_tiles, plan.down_grid)
+        for o in outs[1:]:
+            assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16)), (variant, block_num)
+        assert counters_are_zero(plan, ws), (variant, block_num)
+        res = compare(outs[0].cpu(), golden)
+        assert res["passed"] and res["mean_rel"] <= UNSTAGED_BOUND[dtype], (variant, block_num, res)
+    assert 2 in pieces_seen and max(pieces_seen) >= 3   # tiles of two pieces and of three or more

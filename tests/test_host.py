@@ -129,8 +129,9 @@ def test_streamk_schedule_exact_once_and_slots(G):
                 continue
             kI, dp, sk = n.down_k_iters, n.down_dp_tiles, n.down_sk_tiles
             Gs = n.down_grid      # block_num, or fewer workgroups that cut every tile evenly
+            # every tile split into at most four pieces, equal ones where the iterations allow
             assert Gs <= G and (Gs == G or (n.down_tiles < G and Gs % n.down_tiles == 0
-                                            and kI % (Gs // n.down_tiles) == 0))
+                                            and 2 <= Gs // n.down_tiles <= 4))
             assert dp + sk == n.down_tiles and sk == n.down_tiles % Gs and sk > 0
             total = sk * kI
             q, r = total // Gs, total % Gs
@@ -142,14 +143,17 @@ def test_streamk_schedule_exact_once_and_slots(G):
                 for it in range(a, b):
                     seen[it // kI][it % kI] += 1
             assert all(c == 1 for row in seen for c in row)
-            assert n.workspace_bytes == Gs * n.down_slots_per_wg * n.down_bm * n.down_bn * 4
+            # the fixed region of arrival counters (one per split tile and wave), then the slots
+            counters = _lib.workspace_counter_bytes(n)
+            assert counters == 64 << 10 and sk * _lib.variants()[variant]["waves"] * 4 <= counters
+            assert n.workspace_bytes == counters + Gs * n.down_slots_per_wg * n.down_bm * n.down_bn * 4
 
 
 @pytest.mark.parametrize("G", [8, 37, 256])
 def test_split_up_schedule_covers_once_and_shares_every_tile(G):
     """A split up GEMM (tiles filling at most half the grid, 16 or more K-iterations) covers
     every (tile, K-iteration) exactly once, shares every tile between two or more workgroups
-    (the fixup, not the GEMM, applies its GELU), and its slots fit the workspace (brute force).
+    (its last piece applies the GELU), and its slots fit the workspace (brute force).
     Other up GEMMs keep one workgroup per tile."""
     lib = _lib.load()
     split_seen = 0
@@ -178,7 +182,8 @@ def test_split_up_schedule_covers_once_and_shares_every_tile(G):
                     owners[it // kI].add(v)
             assert all(c == 1 for row in seen for c in row)
             assert all(len(o) >= 2 for o in owners)
-            assert n.workspace_bytes >= Gs * n.up_slots_per_wg * n.up_bm * n.up_bn * 4
+            assert n.workspace_bytes >= (_lib.workspace_counter_bytes(n)
+                                         + Gs * n.up_slots_per_wg * n.up_bm * n.up_bn * 4)
     assert split_seen > 0
 
 
