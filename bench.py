@@ -173,15 +173,8 @@ def traffic_from_profiles(kernel_tag, case_id):
     if not path.exists():
         return None
     text = path.read_text()
-    # the Stream-K down stage is two launches (split GEMM, fixup): its traffic is their sum
-    tags = [kernel_tag] + ([kernel_tag + "_fixup"] if kernel_tag == "down_streamk" else [])
-    total = 0.0
-    for tag in tags:
-        m = re.search(r"^hbm_bytes_per_launch\[" + re.escape(tag) + r"\]:\s*([0-9.eE+]+)", text, re.M)
-        if not m:
-            return None
-        total += float(m.group(1))
-    return total
+    m = re.search(r"^hbm_bytes_per_launch\[" + re.escape(kernel_tag) + r"\]:\s*([0-9.eE+]+)", text, re.M)
+    return float(m.group(1)) if m else None
 
 
 def cpu_baseline(case, budget_s):

@@ -235,10 +235,9 @@ bool split_up(const Variant& v, long long m_valid, long long N, long long K, int
 }
 
 // Up-GEMM tile when none is forced: every variant is priced as the plan it would get, split
-// along K (Stream-K cost, fixup included) or one workgroup per tile.
+// along K (Stream-K cost, the finish of split tiles included) or one workgroup per tile.
 // A SwiGLU up GEMM (N = 2 x the hidden width, gate and up rows interleaved in 32-row blocks)
-// needs wave tiles of whole block pairs and is never split (a split tile's blocks would be
-// finished one by one by the fixup, apart from their partners).
+// needs wave tiles of whole block pairs, and is never split: no split role is compiled for it.
 bool swiglu_tile(const Variant& v) { return (v.bn / v.wgn) % 64 == 0; }
 
 int pick_up(long long M, long long m_valid, long long N, long long K, int G, bool swiglu) {
@@ -621,7 +620,8 @@ int run_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, const voi
         gp.a_bytes = (unsigned)x_span;
     }
     if (split) {
-        // every tile split (no whole tiles): FP32 partials, then the fixup with the activation
+        // every tile split (no whole tiles): FP32 partials; the last piece of a tile applies the
+        // activation
         const long long total = (long long)plan->up_sk_tiles * plan->up_k_iters;
         gp.dp_tiles = 0;
         gp.sk_tiles = plan->up_sk_tiles;

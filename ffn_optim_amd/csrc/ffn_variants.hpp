@@ -43,7 +43,8 @@
 
 
 // launch roles of one variant
-// (the split up roles: every tile split along K, FP32 partials, the GELU applied in the fixup)
+// (the split up roles: tiles split along K, FP32 partials, the activation applied by the last
+// piece of each tile)
 enum {
     FFN_ROLE_UP_ERF = 0,
     FFN_ROLE_UP_RATIONAL = 1,

@@ -14,7 +14,7 @@ import math
 import statistics
 from pathlib import Path
 
-FFN_KERNEL = "ffn_"   # kernel-name fragment of every FFN kernel (ffn_gemm_kernel, ffn_sk_reduce_kernel)
+FFN_KERNEL = "ffn_"   # kernel-name fragment of every FFN kernel (ffn_gemm_kernel)
 
 
 def time_prepared(prepared, warmup=5, repeats=20, *, progress=None):
@@ -109,10 +109,9 @@ def _rows(path):
 
 
 def kernels_per_run(plan):
-    """Kernel launches of one FFN under a plan: the up GEMM, its fixup when the up GEMM is
-    split along K, the down GEMM, and its fixup for Stream-K."""
-    n = plan.native
-    return 2 + (1 if n.up_sk_tiles > 0 else 0) + (1 if n.down_sk_tiles > 0 else 0)
+    """Kernel launches of one FFN under a plan: the up GEMM and the down GEMM.  A split up GEMM
+    and a Stream-K down finish their split tiles inside the same launch."""
+    return 2
 
 
 def _group_runs(rows, per_run):

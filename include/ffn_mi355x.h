@@ -78,9 +78,9 @@ typedef struct ffn_mi355x_plan {
     int ldx, ldw1, ldw2;         /* row pitches, in elements, of X, W1 and W2 */
     /* Split up GEMM.  When its tiles fill at most half of block_num and it is at least 16
        iterations deep, every up tile is split along K over up_grid workgroups: FP32 partials
-       in the workspace, then a fixup that sums them in K order, applies the GELU and stores
-       hidden.  up_sk_tiles = 0: one workgroup per tile.  workspace_bytes covers both GEMMs
-       (they run one after the other on the stream). */
+       in the workspace, and the last piece of each tile to finish sums them in K order,
+       applies the GELU and stores hidden.  up_sk_tiles = 0: one workgroup per tile.
+       workspace_bytes covers both GEMMs (they run one after the other on the stream). */
     int up_k_iters;              /* BK-deep iterations along K per up tile */
     int up_sk_tiles;             /* up tiles split along K (0 or up_tiles) */
     int up_slots_per_wg;         /* FP32 partial-tile slots per workgroup of the split up */

@@ -145,8 +145,8 @@ def test_up_integer_activation_all_variants(dtype, activation):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_down_integer_bias_bit_exact(dtype):
     """Integer hidden, W2 and bias2: out = hidden W2^T + b2 is exact in FP32 and rounded once, for
-    Basic and Stream-K on every variant (the bias enters the register, staged-store and fixup
-    epilogues alike)."""
+    Basic and Stream-K on every variant (the bias enters the register, staged-store and split-tile
+    finish epilogues alike)."""
     lib = _lib.load()
     gen = torch.Generator().manual_seed(13)
     mp, hp, np_ = 320, 1024, 448

@@ -131,37 +131,35 @@ def test_summary_reads_rocprof_outputs(tmp_path):
 
 
 def test_summary_groups_runs_by_launch_count(tmp_path):
-    """A split up GEMM and a Stream-K down GEMM can be the same kernel instantiation (the
-    decode shard: both tile variant 8, both fast-DMA).  Grouping by name recurrence would
-    count every FFN as two runs; grouping by the plan's launch count does not."""
+    """The up and down GEMMs can be the same kernel instantiation (a split up GEMM and a
+    Stream-K down on one tile variant, both fast-DMA).  Grouping by name recurrence would count
+    every FFN as two runs; grouping by the plan's launch count does not."""
     from ffn_optim_amd.performance.collect import extract_summary
     gemm = "void ffn::ffn_gemm_kernel<1, V8, 2, true, true>(ffn::GemmParams)"
-    fix_up = "void ffn::ffn_sk_reduce_kernel<1, V8, 0>(ffn::GemmParams, int)"
-    fix_dn = "void ffn::ffn_sk_reduce_kernel<1, V8, 2>(ffn::GemmParams, int)"
     lines, t = [], 0
     for run in range(3):
-        for name, dur in ((gemm, 12), (fix_up, 2), (gemm, 9), (fix_dn, 3)):
+        for name, dur in ((gemm, 14), (gemm, 12)):
             lines.append(f'"K",{len(lines) + 1},"{name}",{t},{t + dur * 1000}')
             t += dur * 1000 + 500
     _write(tmp_path / "kt" / "x_kernel_trace.csv",
            '"Kind","Dispatch_Id","Kernel_Name","Start_Timestamp","End_Timestamp"\n' + "\n".join(lines) + "\n")
-    assert extract_summary(tmp_path, kernels_per_run=4)["task_duration_us"] == pytest.approx(26.0)
+    assert extract_summary(tmp_path, kernels_per_run=2)["task_duration_us"] == pytest.approx(26.0)
     assert extract_summary(tmp_path)["task_duration_us"] == pytest.approx(13.0)  # the miscount: halves of FFNs
 
 
-def test_kernels_per_run_counts_fixups():
+def test_kernels_per_run_is_two_launches():
+    """Split tiles (a split up GEMM, a Stream-K down) are finished inside their GEMM's launch."""
     from types import SimpleNamespace as NS
     from ffn_optim_amd.performance.collect import kernels_per_run
     assert kernels_per_run(NS(native=NS(up_sk_tiles=0, down_sk_tiles=0))) == 2
-    assert kernels_per_run(NS(native=NS(up_sk_tiles=27, down_sk_tiles=80))) == 4
-    assert kernels_per_run(NS(native=NS(up_sk_tiles=0, down_sk_tiles=80))) == 3
+    assert kernels_per_run(NS(native=NS(up_sk_tiles=27, down_sk_tiles=80))) == 2
 
 
 def test_summary_falls_back_to_kernel_stats(tmp_path):
     from ffn_optim_amd.performance.collect import extract_summary
     _write(tmp_path / "kt_kernel_stats.csv",
            '"Name","Calls","AverageNs"\n"void ffn::ffn_gemm_kernel<1, A, 0, false>(p)",3,40000\n'
-           '"void ffn::ffn_sk_reduce_kernel<1, A>(p)",3,5000\n"void other(int)",1,99999999\n')
+           '"void ffn::ffn_gemm_kernel<1, A, 2, true>(p)",3,5000\n"void other(int)",1,99999999\n')
     assert extract_summary(tmp_path)["task_duration_us"] == pytest.approx(45.0)
 
 

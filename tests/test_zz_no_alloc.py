@@ -5,7 +5,8 @@ no-allocation entry point keeps its partial tiles in the library's own device sc
 every call on the GPU shares: three calls in a row, each smaller than the one before, must
 each match ffn_mi355x_run on a workspace of its own (a stale partial of the previous call
 would show).  The calls cover the Stream-K down (partials) and a split up GEMM (partials, the
-GELU in the fixup).
+GELU applied by the last piece of each tile); a call that left the scratch's arrival counters
+nonzero would break the next.
 """
 import ctypes
 
