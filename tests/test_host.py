@@ -549,13 +549,13 @@ def test_compile_kernel_binds_a_plan_without_a_device():
 # The tile each measured workload runs on, as the design notes' tile table states it:
 # (case id, down path) -> (up variant, down variant).
 TUNED_ASSIGNMENTS = {
-    ("c5_dit_bf16", "basic"): (12, 1), ("c5_dit_bf16", "streamk"): (12, 0),
+    ("c5_dit_bf16", "basic"): (12, 1), ("c5_dit_bf16", "streamk"): (12, 12),
     ("c2_aligned_bf16", "basic"): (12, 13), ("c2_aligned_bf16", "streamk"): (12, 1),
     ("c3_unaligned_fp16", "basic"): (13, 16), ("c3_unaligned_fp16", "streamk"): (13, 5),
-    ("c4_decode_bf16", "basic"): (14, 15), ("c4_decode_bf16", "streamk"): (14, 14),
-    ("c1_smoke_fp16", "basic"): (4, 15), ("c1_smoke_fp16", "streamk"): (4, 4),
-    ("c5_tp8_shard_bf16", "basic"): (0, 1), ("c5_tp8_shard_bf16", "streamk"): (13, 12),
-    ("c4_tp8_shard_bf16", "basic"): (15, 15), ("c4_tp8_shard_bf16", "streamk"): (15, 14),
+    ("c4_decode_bf16", "basic"): (14, 15), ("c4_decode_bf16", "streamk"): (8, 14),
+    ("c1_smoke_fp16", "basic"): (4, 15), ("c1_smoke_fp16", "streamk"): (4, 15),
+    ("c5_tp8_shard_bf16", "basic"): (12, 1), ("c5_tp8_shard_bf16", "streamk"): (12, 12),
+    ("c4_tp8_shard_bf16", "basic"): (15, 15), ("c4_tp8_shard_bf16", "streamk"): (15, 16),
 }
 
 
