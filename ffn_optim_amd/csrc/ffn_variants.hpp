@@ -16,8 +16,11 @@
 // tiles over half of every stage): two MFMAs per k-step per wave instead of one, for the
 // latency-bound down GEMMs with one 64x64 tile per CU (-8 to -9% on the unaligned mid-size
 // and the decode Basic down).
-// Each variant is built for both storage types and four epilogues (GELU-erf,
-// GELU-rational, plain store, plain store + Stream-K split) in its own object.
+// Each variant is built for both storage types in its own object, with every launch role:
+// the up epilogues (GELU-erf, GELU-rational, SiLU, and SwiGLU where its wave tiles hold whole
+// 64-column block pairs), the plain store of the down GEMM, the Stream-K form of the store and
+// of the GELU / SiLU up (split tiles finished in the launch), and gathered-row forms of the up
+// roles for an X read in place as a strided view.
 #pragma once
 
 #define FFN_VARIANTS(X)                     \
