@@ -33,6 +33,6 @@ def report(records, best):
               "- A best configuration holds only for this case, input, device, library revision and search space.",
               "- Pipeline utilisation comes only from collected counters (rocprofv3 --pmc); "
               "it is reported as unavailable otherwise, never estimated from totals.",
-              "- The FFN is two (Basic) or three (Stream-K) kernels; a step time is not split into "
+              "- The FFN is two kernels (up, down); a step time is not split into "
               "up, GELU and down from event timing alone.", ""]
     return "\n".join(lines)
