@@ -171,3 +171,20 @@ def test_down_integer_bias_bit_exact(dtype):
             assert counters_are_zero(plan, ws), (variant, down, block_num)
             say("down-bias", dtype, variant, down, block_num)
             assert torch.equal(out.cpu().view(torch.int16), golden.view(torch.int16)), (variant, down, block_num)
+
+
+@pytest.mark.parametrize("activation", ["gelu", "silu", "swiglu"])
+def test_eagle_permuted_x_read_in_place(activation):
+    """eagle_ffn_linear on a permuted X (a [97, 3, 200] view of a [3, 97, 200] tensor) reads its
+    rows in place through the row grid, biases and every activation included: bit-identical to
+    the same call on a contiguous copy of X, and within the criterion of the golden."""
+    from ffn_optim_amd.host.inputs import row_grid
+    x, w1, w2, b1, b2 = _inputs((3, 97), 200, 320, 136, torch.bfloat16, activation, True, 7)
+    dev = [t.cuda() for t in (x, w1, w2, b1, b2)]
+    xt = dev[0].transpose(0, 1)
+    assert row_grid(xt, 200)[0] == "grid"
+    out = eagle_ffn_linear(xt, *dev[1:], activation=activation)
+    ref = eagle_ffn_linear(xt.contiguous(), *dev[1:], activation=activation)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), activation
+    _check(out, x.transpose(0, 1), w1, w2, b1, b2, activation, f"{activation} permuted X")
