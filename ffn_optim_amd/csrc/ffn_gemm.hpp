@@ -734,14 +734,18 @@ struct Engine {
     }
 
     // acc = sum over K-iterations [u.kb, u.ke) of tile (u.tm, u.tn).  On entry the DMA prologue
-    // of the unit is in flight, possibly behind the previous unit's stores, so the first wait
-    // drains everything.  Iteration it fetches iteration it+S-1 into the stage freed at the end
+    // of the unit is in flight (behind the previous unit's stores but for the first unit), and
+    // the first wait takes stage 0 (first unit) or drains everything.  Iteration it fetches iteration it+S-1 into the stage freed at the end
     // of it-1; past the end of the unit it issues the same DMA with out-of-range offsets
     // (zeros into the free stage), which keeps every stage wait a compile-time count.  The
     // last iteration starts the DMA prologue of `nx`, which then overlaps this unit's epilogue.
+    // `first`: the workgroup's first unit, whose DMA prologue has no stores behind it; its first
+    // iteration then waits for stage 0 alone instead of the whole prologue.  (Behind a later
+    // unit's prologue lie the previous unit's output stores, which the load count cannot
+    // order against, so that unit waits for everything.)
     template <bool FASTK>
     __device__ __forceinline__ void mainloop(const GemmParams& p, const Unit& u, const Unit& nx,
-                                             f32x16 (&acc)[FN][FM]) {
+                                             f32x16 (&acc)[FN][FM], bool first = false) {
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
@@ -750,7 +754,8 @@ struct Engine {
         rsrc(p, u, ra, rb);
         const DmaLane L = dma_lane(p, u);
         const int n = u.ke - u.kb;
-        wait_vmcnt<0>();
+        if (first) wait_vmcnt<C::LOADS * (S - 2)>();
+        else wait_vmcnt<0>();
         barrier();
         read_a_range<0, 0, FM>(0, 0);
         read_b_range<0, FN>(0, 0);
@@ -1226,9 +1231,11 @@ __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
     Unit u = walk.next(p);
     if (!u.valid) return;
     eng.prologue(p, u);
+    bool first = true;
     while (true) {
         const Unit nx = walk.next(p);
-        eng.template mainloop<FASTK>(p, u, nx, acc);
+        eng.template mainloop<FASTK>(p, u, nx, acc, first);
+        first = false;
         if (SK && u.split >= 0)
             eng.template finish_split<EPI>(p, u, v, nx.valid, acc);
         else if constexpr (C::WGK > 1)
