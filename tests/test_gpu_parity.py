@@ -102,7 +102,8 @@ def test_prepared_run_replays_from_a_captured_graph(case_id, down):
     """PreparedFFN.run() allocates, clears and synchronises nothing, so a caller can capture it in
     a HIP graph (prepared on the capture stream, which run() checks).  Every replay, with eager
     work on the output in between, matches the eager result bit for bit.  The decode shard's
-    plan splits its up GEMM (three launches)."""
+    plan splits its up GEMM and the Stream-K plans split down tiles: their arrival counters must
+    be left zero by every replay for the next one to sum correctly."""
     case = get_case(case_id)
     x, w1, w2 = make_inputs(case, "cuda")
     eager = prepare_ffn(x, w1, w2, down_impl=down).run().clone()
