@@ -83,7 +83,7 @@ struct GemmParams {
 // WTM x WTN wave tile over its own BK/WGK slice of every stage, and the WGK partial tiles are
 // summed through LDS after the main loop.
 template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int STAGES_, int SYNCQ_ = -1, int DMAKS_ = -1,
-          int WGK_ = 1>
+          int WGK_ = 1, int DMAW_ = 0>
 struct TileCfg {
     static constexpr int BM = BM_, BN = BN_, BK = BK_;
     static constexpr int WGM = WGM_, WGN = WGN_, WGK = WGK_, STAGES = STAGES_;
@@ -102,8 +102,14 @@ struct TileCfg {
     static constexpr int A_BYTES = BM * ROWB, B_BYTES = BN * ROWB;
     static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
     static constexpr int A_BLKS = A_BYTES / 1024, B_BLKS = B_BYTES / 1024;
-    static constexpr int A_PW = A_BLKS / NW, B_PW = B_BLKS / NW;  // DMA blocks per wave
-    static constexpr int LOADS = A_PW + B_PW;      // DMA instructions per wave per stage
+    // Waves issuing the refill DMA: all of them (DMAW_ = 0) or waves [0, DMAW_).  A workgroup's
+    // waves w and w + 4 share a SIMD (HW_REG_HW_ID read back on gfx950), so with eight waves
+    // and DMAW_ = 4 every SIMD holds one wave that refills and one that only reads LDS and
+    // issues MFMAs: while the first waits on the texture unit, the second keeps the matrix
+    // core busy.
+    static constexpr int DW = DMAW_ == 0 ? NW : DMAW_;
+    static constexpr int A_PW = A_BLKS / DW, B_PW = B_BLKS / DW;  // DMA blocks per issuing wave
+    static constexpr int LOADS = A_PW + B_PW;      // DMA instructions per issuing wave per stage
     static constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
     static constexpr int KSTEPS = BK / 16 / WGK;   // MFMA k-steps per stage and wave
     // Output staging of the epilogue: from stage STAGES-1 (which the next unit's DMA prologue
@@ -129,7 +135,8 @@ struct TileCfg {
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
     static_assert(ROWB % 16 == 0 && CH >= 2, "BK must be a multiple of 16");
     static_assert(BK % (16 * WGK) == 0, "every wave takes whole k-steps of a stage");
-    static_assert(A_BLKS % NW == 0 && B_BLKS % NW == 0, "DMA blocks must split evenly over waves");
+    static_assert(NW % DW == 0 && A_BLKS % DW == 0 && B_BLKS % DW == 0,
+                  "DMA blocks must split evenly over the issuing waves");
     static_assert(32 % (CH * R256) == 0, "fragment rows start on a swizzle period");
     // DMA offset sets a lane keeps: one per block of the swizzle period (at least two)
     static constexpr int NPAR = SWZ_PERIOD > 2 ? SWZ_PERIOD : 2;
@@ -390,7 +397,8 @@ struct UnitWalker {
 // the GEMM engine
 // ---------------------------------------------------------------------------
 
-template <int DT, class C, bool GA = false>
+// ISSUE: this wave issues its share of the refill DMA (false for the waves at or past C::DW).
+template <int DT, class C, bool GA = false, bool ISSUE = true>
 struct Engine {
     static constexpr int FM = C::FM, FN = C::FN, NT = C::NT, S = C::STAGES, KS = C::KSTEPS;
     static_assert(KS % 2 == 0, "fragment double-buffer assumes an even number of k-steps per wave");
@@ -455,7 +463,7 @@ struct Engine {
             // the row of each A instruction, decomposed over the gathered grid once per unit
 #pragma unroll
             for (int D = 0; D < C::A_PW; ++D) {
-                const int r = u.tm * C::BM + (wave * C::A_PW + D) * C::RPB + rl;
+                const int r = u.tm * C::BM + ((ISSUE ? wave : 0) * C::A_PW + D) * C::RPB + rl;
                 const unsigned i2 = (unsigned)r % (unsigned)p.a_d2, t = (unsigned)r / (unsigned)p.a_d2;
                 const unsigned i1 = t % (unsigned)p.a_d1, i0 = t / (unsigned)p.a_d1;
                 const unsigned e = i0 * (unsigned)p.a_s0 + i1 * (unsigned)p.a_s1 + i2 * (unsigned)p.a_s2;
@@ -546,18 +554,19 @@ struct Engine {
             issue_range_impl<FAST, D0 + 1, D1>(p, ra, rb, stage, L, t);
         }
     }
+
     // (gathered rows always take the checked path: the host launches them without FASTK)
     template <bool FAST, int D0, int D1>
     __device__ __forceinline__ void issue_range(const GemmParams& p, const __amdgpu_buffer_rsrc_t& ra,
                                                 const __amdgpu_buffer_rsrc_t& rb, int stage,
                                                 const DmaLane& L, const DmaIt& t) const {
-        issue_range_impl<FAST && !GA, D0, D1>(p, ra, rb, stage, L, t);
+        if constexpr (ISSUE) issue_range_impl<FAST && !GA, D0, D1>(p, ra, rb, stage, L, t);
     }
 
     // K-iterations 0..S-2 of a unit go to stages 0..S-2; iteration S-1+it is fetched during
     // iteration it.  A unit shorter than S-1 iterations still issues all S-1 stages (zeros past
-    // its end): the epilogue then knows that exactly the last LOADS*(S-1) loads of a wave
-    // belong to the next unit, and that every load before them -- the zero fills of the
+    // its end): the epilogue then knows that exactly the last LOADS*(S-1) loads of an issuing
+    // wave belong to the next unit, and that every load before them -- the zero fills of the
     // current unit's last iterations included -- has to land before the staging area is
     // written.
     __device__ __forceinline__ void prologue(const GemmParams& p, const Unit& u) const {
@@ -1192,41 +1201,23 @@ struct Engine {
     }
 };
 
-// Persistent GEMM: every workgroup walks its units (whole tiles, then for Stream-K its split
-// iterations) with the DMA of the next unit overlapping the epilogue of the current one.
-// Split pieces that share a tile publish FP32 partials; the last to arrive finishes the tile.
-template <int DT, class C, int EPI, bool SK, bool FASTK, bool GATHER = false>
-__global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
-    // The activation epilogue stores from registers, where its VALU work overlaps the stores;
-    // the plain cast stages through LDS, whose full-row stores drain faster when every
-    // workgroup stores at once.  The Stream-K kernel, whose split pieces leave through
-    // store_partial, stores its whole tiles from registers too: the staging registers would
-    // push it past 256 VGPRs.
-    // A K-sliced tile exchanges its partial sums through the free stage(s) and stores from
-    // registers; its Stream-K pieces exchange first and then store their FP32 partials.
-    constexpr bool EPI_IN_REGS = EPI != EPI_STORE || SK;
-    constexpr int SMEM = C::WGK > 1 ? C::LDS_USE : EPI_IN_REGS ? C::LDS_BYTES : C::LDS_ALLOC;
-    __shared__ __attribute__((aligned(1024))) char smem_raw[SMEM];
-    static_assert(!(GATHER && FASTK), "gathered rows take the checked refill path");
-    Engine<DT, C, GATHER> eng((lds_char*)smem_raw, p);
+// The activation epilogue stores from registers, where its VALU work overlaps the stores;
+// the plain cast stages through LDS, whose full-row stores drain faster when every
+// workgroup stores at once.  The Stream-K kernel, whose split pieces leave through
+// store_partial, stores its whole tiles from registers too: the staging registers would
+// push it past 256 VGPRs.
+// A K-sliced tile exchanges its partial sums through the free stage(s) and stores from
+// registers; its Stream-K pieces exchange first and then store their FP32 partials.
+template <int EPI, bool SK>
+constexpr bool epi_in_regs() { return EPI != EPI_STORE || SK; }
+
+// One wave's walk over its workgroup's units, in the refill role ISSUE.  Every wave of the
+// workgroup passes the same barriers whatever its role.
+template <int DT, class C, int EPI, bool SK, bool FASTK, bool GATHER, bool ISSUE>
+__device__ __forceinline__ void walk_units(const GemmParams& p, lds_char* smem, int v, int G) {
+    constexpr bool EPI_IN_REGS = epi_in_regs<EPI, SK>();
+    Engine<DT, C, GATHER, ISSUE> eng(smem, p);
     f32x16 acc[C::FN][C::FM];
-
-    const int G = gridDim.x;
-    const int g = blockIdx.x;
-    // Workgroups are dispatched round-robin over the 8 XCDs; renumber them so that
-    // consecutive virtual ids (which take neighbouring tiles) share one XCD's L2.
-    const int v = ((G & 7) == 0) ? (g & 7) * (G >> 3) + (g >> 3) : g;
-
-    // Output rows past the last tile row that holds data (zero padding of a small-M problem) are
-    // not computed: every workgroup writes its share of them as zeros, ahead of its first unit.
-    if (p.zero_row0 < p.M) {
-        const int cpr = p.c_cols / 8;  // 16-byte chunks per row
-        const long long total = (long long)(p.M - p.zero_row0) * cpr;
-        for (long long i = (long long)g * C::NT + threadIdx.x; i < total; i += (long long)G * C::NT) {
-            const long long r = p.zero_row0 + i / cpr, c = i % cpr;
-            *(u32x4*)((char*)p.c + ((size_t)r * (size_t)p.ldc + (size_t)c * 8) * 2) = u32x4{0u, 0u, 0u, 0u};
-        }
-    }
     UnitWalker<SK> walk(p, v, G);
     Unit u = walk.next(p);
     if (!u.valid) return;
@@ -1247,6 +1238,40 @@ __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
         if (!nx.valid) break;
         u = nx;
     }
+}
+
+// Persistent GEMM: every workgroup walks its units (whole tiles, then for Stream-K its split
+// iterations) with the DMA of the next unit overlapping the epilogue of the current one.
+// Split pieces that share a tile publish FP32 partials; the last to arrive finishes the tile.
+template <int DT, class C, int EPI, bool SK, bool FASTK, bool GATHER = false>
+__global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
+    constexpr int SMEM = C::WGK > 1 ? C::LDS_USE : epi_in_regs<EPI, SK>() ? C::LDS_BYTES : C::LDS_ALLOC;
+    __shared__ __attribute__((aligned(1024))) char smem_raw[SMEM];
+    static_assert(!(GATHER && FASTK), "gathered rows take the checked refill path");
+
+    const int G = gridDim.x;
+    const int g = blockIdx.x;
+    // Workgroups are dispatched round-robin over the 8 XCDs; renumber them so that
+    // consecutive virtual ids (which take neighbouring tiles) share one XCD's L2.
+    const int v = ((G & 7) == 0) ? (g & 7) * (G >> 3) + (g >> 3) : g;
+
+    // Output rows past the last tile row that holds data (zero padding of a small-M problem) are
+    // not computed: every workgroup writes its share of them as zeros, ahead of its first unit.
+    if (p.zero_row0 < p.M) {
+        const int cpr = p.c_cols / 8;  // 16-byte chunks per row
+        const long long total = (long long)(p.M - p.zero_row0) * cpr;
+        for (long long i = (long long)g * C::NT + threadIdx.x; i < total; i += (long long)G * C::NT) {
+            const long long r = p.zero_row0 + i / cpr, c = i % cpr;
+            *(u32x4*)((char*)p.c + ((size_t)r * (size_t)p.ldc + (size_t)c * 8) * 2) = u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+    lds_char* smem = (lds_char*)smem_raw;
+    if constexpr (C::DW == C::NW)
+        walk_units<DT, C, EPI, SK, FASTK, GATHER, true>(p, smem, v, G);
+    else if (__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) < C::DW)
+        walk_units<DT, C, EPI, SK, FASTK, GATHER, true>(p, smem, v, G);
+    else
+        walk_units<DT, C, EPI, SK, FASTK, GATHER, false>(p, smem, v, G);
 }
 
 }  // namespace ffn

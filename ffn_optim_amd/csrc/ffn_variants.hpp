@@ -1,7 +1,7 @@
 // ffn_variants.hpp -- the macro-tile variants compiled into libffn_mi355x.so.
 //
 // X(id, BM, BN, BK, waves along M, waves along N, LDS stages[, sync slot, DMA k-steps,
-//   waves along K])
+//   waves along K, waves issuing the refill])
 // (DMA k-steps equal to the k-steps per stage spreads a deep pipeline's refill over the
 // whole iteration.)  The K-sliced 128x128 tiles (10, 11) give each wave a 128x64 wave tile
 // over half of every stage: a quarter fewer fragment reads per MFMA than 64x64 wave tiles,
@@ -10,7 +10,9 @@
 // the other's LDS and barrier waits.  Variant 12 runs the
 // 256x256 tile with eight waves (two per SIMD, 128x64 wave tiles): when every CU holds a
 // single tile, the second wave of a SIMD issues MFMAs while the first waits on LDS or DMA.
-// Its refill goes out in the first k-step of the iteration (2% faster on the DiT-size up).
+// Its refill goes out in the first k-step of the iteration (2% faster on the DiT-size up),
+// issued by waves 0-3 alone, one per SIMD (2-4% faster on the DiT-size GEMMs than all
+// eight waves sharing it).
 // The deep-pipeline 64-row tiles (8, 9) keep 56 KiB or more of weights in flight per CU for
 // the memory-bound small-M (decode) shapes.  Variant 14 K-slices the 64x64 tile (64x32 wave
 // tiles over half of every stage): two MFMAs per k-step per wave instead of one, for the
@@ -36,7 +38,7 @@
     X(9, 64, 128, 64, 2, 2, 6)              \
     X(10, 128, 128, 64, 1, 2, 5, -1, 2, 2)  \
     X(11, 128, 128, 64, 1, 2, 4, -1, 2, 2)  \
-    X(12, 256, 256, 64, 2, 4, 2, -1, 1)     \
+    X(12, 256, 256, 64, 2, 4, 2, -1, 1, 1, 4) \
     X(13, 128, 128, 64, 2, 2, 4, 3, 2, 2)   \
     X(14, 64, 64, 64, 1, 2, 6, -1, 2, 2)    \
     X(15, 32, 32, 128, 1, 1, 8, -1, 4, 2)   \
