@@ -121,6 +121,9 @@ struct TileCfg {
     static constexpr int EPI_OFF = (STAGES - 1) * STAGE_BYTES;
     static constexpr int EPI_AVAIL = (LDS_BYTES > LDS_MAX / 2) ? LDS_MAX - EPI_OFF : STAGE_BYTES;
     static constexpr int OUT_ROWB = BN * 2;        // bytes of one staged output row (unpadded)
+    // The staged rows' chunk XOR keeps a row's 16-byte pieces inside the row only when their
+    // number is a power of two; other tile widths store from registers.
+    static constexpr bool OUT_POW2 = ((BN / 8) & (BN / 8 - 1)) == 0;
     static constexpr int er_pick() {
         for (int er = BM; er >= 32 * WGM; er /= 2)
             if (BM % er == 0 && (er / WGM) % 32 == 0 && er * OUT_ROWB <= EPI_AVAIL) return er;
@@ -837,6 +840,7 @@ struct Engine {
     template <int EPI, bool BIAS>
     __device__ __forceinline__ void store_tile_lds_as(const GemmParams& p, const Unit& u, bool next,
                                                       f32x16 (&acc)[FN][FM]) {
+        static_assert(C::OUT_POW2, "the staging swizzle needs a power-of-two number of pieces per row");
         lds_char* eb = smem + C::EPI_OFF;
         // DMA still in flight may target any stage but the next unit's prologue (issued last):
         // drain it; the barrier before the first staging write makes sure every wave has
@@ -1207,15 +1211,16 @@ struct Engine {
 // store_partial, stores its whole tiles from registers too: the staging registers would
 // push it past 256 VGPRs.
 // A K-sliced tile exchanges its partial sums through the free stage(s) and stores from
-// registers; its Stream-K pieces exchange first and then store their FP32 partials.
-template <int EPI, bool SK>
-constexpr bool epi_in_regs() { return EPI != EPI_STORE || SK; }
+// registers; its Stream-K pieces exchange first and then store their FP32 partials.  A tile
+// whose output rows are not a power-of-two number of 16-byte pieces stores from registers.
+template <class C, int EPI, bool SK>
+constexpr bool epi_in_regs() { return EPI != EPI_STORE || SK || !C::OUT_POW2; }
 
 // One wave's walk over its workgroup's units, in the refill role ISSUE.  Every wave of the
 // workgroup passes the same barriers whatever its role.
 template <int DT, class C, int EPI, bool SK, bool FASTK, bool GATHER, bool ISSUE>
 __device__ __forceinline__ void walk_units(const GemmParams& p, lds_char* smem, int v, int G) {
-    constexpr bool EPI_IN_REGS = epi_in_regs<EPI, SK>();
+    constexpr bool EPI_IN_REGS = epi_in_regs<C, EPI, SK>();
     Engine<DT, C, GATHER, ISSUE> eng(smem, p);
     f32x16 acc[C::FN][C::FM];
     UnitWalker<SK> walk(p, v, G);
@@ -1245,7 +1250,7 @@ __device__ __forceinline__ void walk_units(const GemmParams& p, lds_char* smem, 
 // Split pieces that share a tile publish FP32 partials; the last to arrive finishes the tile.
 template <int DT, class C, int EPI, bool SK, bool FASTK, bool GATHER = false>
 __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
-    constexpr int SMEM = C::WGK > 1 ? C::LDS_USE : epi_in_regs<EPI, SK>() ? C::LDS_BYTES : C::LDS_ALLOC;
+    constexpr int SMEM = C::WGK > 1 ? C::LDS_USE : epi_in_regs<C, EPI, SK>() ? C::LDS_BYTES : C::LDS_ALLOC;
     __shared__ __attribute__((aligned(1024))) char smem_raw[SMEM];
     static_assert(!(GATHER && FASTK), "gathered rows take the checked refill path");
 
