@@ -58,6 +58,7 @@ SIGNATURES = {
     "ffn_mi355x_down": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp]),
     "ffn_mi355x_num_variants": (_i, []),
     "ffn_mi355x_variant_info": (_i, [_i, _P(_i), _P(_i), _P(_i), _P(_i), _P(_i), _P(_i)]),
+    "ffn_mi355x_variant_refill_waves": (_i, [_i]),
     "ffn_mi355x_last_error": (ctypes.c_char_p, []),
     "ffn_mi355x_strerror": (ctypes.c_char_p, [_i]),
     "ffn_mi355x_version": (ctypes.c_char_p, []),
@@ -161,6 +162,8 @@ def variants() -> list[dict]:
     for v in range(lib.ffn_mi355x_num_variants()):
         vals = [ctypes.c_int(0) for _ in range(6)]
         check(lib.ffn_mi355x_variant_info(v, *map(ctypes.byref, vals)))
+        refill = lib.ffn_mi355x_variant_refill_waves(v)
+        check(min(refill, 0))
         out.append(dict(zip(("bm", "bn", "bk", "waves", "stages", "lds_bytes"),
-                            (x.value for x in vals)), variant=v))
+                            (x.value for x in vals)), variant=v, refill_waves=refill))
     return out

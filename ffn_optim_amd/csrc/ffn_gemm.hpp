@@ -83,13 +83,16 @@ struct GemmParams {
 // WTM x WTN wave tile over its own BK/WGK slice of every stage, and the WGK partial tiles are
 // summed through LDS after the main loop.
 template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int STAGES_, int SYNCQ_ = -1, int DMAKS_ = -1,
-          int WGK_ = 1, int DMAW_ = 0>
+          int WGK_ = 1, int DMAW_ = 0, int PROD_ = 0>
 struct TileCfg {
     static constexpr int BM = BM_, BN = BN_, BK = BK_;
     static constexpr int WGM = WGM_, WGN = WGN_, WGK = WGK_, STAGES = STAGES_;
     static constexpr int SYNCQ = SYNCQ_, DMAKS = DMAKS_;
-    static constexpr int NW = WGM * WGN * WGK;     // waves per workgroup
-    static constexpr int NT = NW * 64;             // threads per workgroup
+    static constexpr int NW = WGM * WGN * WGK;     // waves holding wave tiles
+    // PROD_ > 0: that many more waves (numbered first) only refill the LDS stages; the NW
+    // tile waves then issue no DMA.
+    static constexpr int PROD = PROD_;
+    static constexpr int NT = (NW + PROD) * 64;    // threads per workgroup
     static constexpr int WTM = BM / WGM, WTN = BN / WGN;  // wave tile
     static constexpr int FM = WTM / 32, FN = WTN / 32;    // 32x32 MFMA blocks per wave
     static constexpr int ROWB = BK * 2;            // bytes of one LDS row
@@ -107,7 +110,8 @@ struct TileCfg {
     // and DMAW_ = 4 every SIMD holds one wave that refills and one that only reads LDS and
     // issues MFMAs: while the first waits on the texture unit, the second keeps the matrix
     // core busy.
-    static constexpr int DW = DMAW_ == 0 ? NW : DMAW_;
+    static constexpr int DW = PROD > 0 ? PROD : DMAW_ == 0 ? NW : DMAW_;
+    static_assert(PROD == 0 || (WGK == 1 && DMAW_ == 0), "refill waves serve plain (not K-sliced) tiles");
     static constexpr int A_PW = A_BLKS / DW, B_PW = B_BLKS / DW;  // DMA blocks per issuing wave
     static constexpr int LOADS = A_PW + B_PW;      // DMA instructions per issuing wave per stage
     static constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
@@ -401,7 +405,8 @@ struct UnitWalker {
 // ---------------------------------------------------------------------------
 
 // ISSUE: this wave issues its share of the refill DMA (false for the waves at or past C::DW).
-template <int DT, class C, bool GA = false, bool ISSUE = true>
+// MMA: this wave holds a wave tile (false for the refill waves of a tile with C::PROD > 0).
+template <int DT, class C, bool GA = false, bool ISSUE = true, bool MMA = true>
 struct Engine {
     static constexpr int FM = C::FM, FN = C::FN, NT = C::NT, S = C::STAGES, KS = C::KSTEPS;
     static_assert(KS % 2 == 0, "fragment double-buffer assumes an even number of k-steps per wave");
@@ -416,9 +421,10 @@ struct Engine {
         tid = threadIdx.x;
         lane = tid & 63;
         wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-        wm = wave % C::WGM;
-        wn = C::WGK == 1 ? wave / C::WGM : (wave / C::WGM) % C::WGN;
-        wk = C::WGK == 1 ? 0 : wave / (C::WGM * C::WGN);
+        const int tw = MMA ? wave - C::PROD : 0;  // index among the tile waves
+        wm = tw % C::WGM;
+        wn = C::WGK == 1 ? tw / C::WGM : (tw / C::WGM) % C::WGN;
+        wk = C::WGK == 1 ? 0 : tw / (C::WGM * C::WGN);
         const int r = lane & 31;
         a_row_off = (wm * C::WTM + r) * C::ROWB;
         b_row_off = C::A_BYTES + (wn * C::WTN + r) * C::ROWB;
@@ -592,13 +598,17 @@ struct Engine {
     }
     template <int BUF, int I>
     __device__ __forceinline__ void read_a(int stage, int ks) {
-        const lds_char* st = smem + stage * C::STAGE_BYTES;
-        fa[BUF][I] = *(const __attribute__((address_space(3))) u32x4*)(st + a_row_off + I * 32 * C::ROWB + frag_chunk(ks));
+        if constexpr (MMA) {
+            const lds_char* st = smem + stage * C::STAGE_BYTES;
+            fa[BUF][I] = *(const __attribute__((address_space(3))) u32x4*)(st + a_row_off + I * 32 * C::ROWB + frag_chunk(ks));
+        }
     }
     template <int J>
     __device__ __forceinline__ void read_b(int stage, int ks) {
-        const lds_char* st = smem + stage * C::STAGE_BYTES;
-        fb[J] = *(const __attribute__((address_space(3))) u32x4*)(st + b_row_off + J * 32 * C::ROWB + frag_chunk(ks));
+        if constexpr (MMA) {
+            const lds_char* st = smem + stage * C::STAGE_BYTES;
+            fb[J] = *(const __attribute__((address_space(3))) u32x4*)(st + b_row_off + J * 32 * C::ROWB + frag_chunk(ks));
+        }
     }
     template <int BUF, int I0, int I1>
     __device__ __forceinline__ void read_a_range(int stage, int ks) {
@@ -669,7 +679,7 @@ struct Engine {
                                          const __amdgpu_buffer_rsrc_t& ra, const __amdgpu_buffer_rsrc_t& rb,
                                          int dma_stage, const DmaLane& L, const DmaIt& o, const Unit& nx) {
         constexpr int j = Q / FM, i = Q % FM;
-        acc[j][i] = mfma32<DT>(fb[j], fa[CB][i], acc[j][i]);
+        if constexpr (MMA) acc[j][i] = mfma32<DT>(fb[j], fa[CB][i], acc[j][i]);
         constexpr int NB = 1 - CB;
         if constexpr (MODE == 0) {
             // A fragments of the next k-step over the first half of the slots; B fragment j
@@ -758,10 +768,12 @@ struct Engine {
     template <bool FASTK>
     __device__ __forceinline__ void mainloop(const GemmParams& p, const Unit& u, const Unit& nx,
                                              f32x16 (&acc)[FN][FM], bool first = false) {
+        if constexpr (MMA) {
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
+            for (int j = 0; j < FN; ++j)
 #pragma unroll
-            for (int i = 0; i < FM; ++i) acc[j][i] = f32x16{};
+                for (int i = 0; i < FM; ++i) acc[j][i] = f32x16{};
+        }
         __amdgpu_buffer_rsrc_t ra, rb;
         rsrc(p, u, ra, rb);
         const DmaLane L = dma_lane(p, u);
@@ -1212,16 +1224,19 @@ struct Engine {
 // push it past 256 VGPRs.
 // A K-sliced tile exchanges its partial sums through the free stage(s) and stores from
 // registers; its Stream-K pieces exchange first and then store their FP32 partials.  A tile
-// whose output rows are not a power-of-two number of 16-byte pieces stores from registers.
+// whose output rows are not a power-of-two number of 16-byte pieces stores from registers, and
+// so does a tile with refill waves (which hold no output).
 template <class C, int EPI, bool SK>
-constexpr bool epi_in_regs() { return EPI != EPI_STORE || SK || !C::OUT_POW2; }
+constexpr bool epi_in_regs() { return EPI != EPI_STORE || SK || !C::OUT_POW2 || C::PROD > 0; }
 
-// One wave's walk over its workgroup's units, in the refill role ISSUE.  Every wave of the
-// workgroup passes the same barriers whatever its role.
-template <int DT, class C, int EPI, bool SK, bool FASTK, bool GATHER, bool ISSUE>
+// One wave's walk over its workgroup's units, in the refill role ISSUE and tile role MMA.
+// Every wave of the workgroup passes the same barriers whatever its roles.
+template <int DT, class C, int EPI, bool SK, bool FASTK, bool GATHER, bool ISSUE, bool MMA = true>
 __device__ __forceinline__ void walk_units(const GemmParams& p, lds_char* smem, int v, int G) {
     constexpr bool EPI_IN_REGS = epi_in_regs<C, EPI, SK>();
-    Engine<DT, C, GATHER, ISSUE> eng(smem, p);
+    // the refill waves skip the epilogue, which therefore may hold no barrier
+    static_assert(C::PROD == 0 || (!SK && EPI_IN_REGS && C::WGK == 1), "refill waves: barrier-free epilogue only");
+    Engine<DT, C, GATHER, ISSUE, MMA> eng(smem, p);
     f32x16 acc[C::FN][C::FM];
     UnitWalker<SK> walk(p, v, G);
     Unit u = walk.next(p);
@@ -1232,14 +1247,16 @@ __device__ __forceinline__ void walk_units(const GemmParams& p, lds_char* smem, 
         const Unit nx = walk.next(p);
         eng.template mainloop<FASTK>(p, u, nx, acc, first);
         first = false;
-        if (SK && u.split >= 0)
-            eng.template finish_split<EPI>(p, u, v, nx.valid, acc);
-        else if constexpr (C::WGK > 1)
-            eng.template store_sliced<EPI>(p, u, nx.valid, acc);
-        else if constexpr (EPI_IN_REGS)
-            eng.template store_tile_regs<EPI>(p, u, acc);
-        else
-            eng.template store_tile_lds<EPI>(p, u, nx.valid, acc);
+        if constexpr (MMA) {
+            if (SK && u.split >= 0)
+                eng.template finish_split<EPI>(p, u, v, nx.valid, acc);
+            else if constexpr (C::WGK > 1)
+                eng.template store_sliced<EPI>(p, u, nx.valid, acc);
+            else if constexpr (EPI_IN_REGS)
+                eng.template store_tile_regs<EPI>(p, u, acc);
+            else
+                eng.template store_tile_lds<EPI>(p, u, nx.valid, acc);
+        }
         if (!nx.valid) break;
         u = nx;
     }
@@ -1271,7 +1288,12 @@ __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
         }
     }
     lds_char* smem = (lds_char*)smem_raw;
-    if constexpr (C::DW == C::NW)
+    if constexpr (C::PROD > 0) {
+        if (__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) < C::PROD)
+            walk_units<DT, C, EPI, SK, FASTK, GATHER, true, false>(p, smem, v, G);
+        else
+            walk_units<DT, C, EPI, SK, FASTK, GATHER, false, true>(p, smem, v, G);
+    } else if constexpr (C::DW == C::NW)
         walk_units<DT, C, EPI, SK, FASTK, GATHER, true>(p, smem, v, G);
     else if (__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) < C::DW)
         walk_units<DT, C, EPI, SK, FASTK, GATHER, true>(p, smem, v, G);

@@ -41,10 +41,11 @@ namespace {
 struct Variant {
     int bm, bn, bk, wgm, wgn, stages;
     int lds_bytes;            // LDS of one workgroup: the stages plus any epilogue staging beyond
-    int nw;                   // waves per workgroup
+    int nw;                   // waves holding wave tiles
     int wgk;                  // waves along K (K-sliced tile when > 1)
+    int prod;                 // waves that only refill the LDS stages (whole tiles only when > 0)
     ffn_launch_fn launch[2];  // [dtype]
-    int waves() const { return nw; }
+    int waves() const { return nw + prod; }
     int lds() const { return lds_bytes; }
 };
 
@@ -52,6 +53,7 @@ struct Variant {
     {bm, bn, bk, wgm, wgn, st, ffn::TileCfg<bm, bn, bk, wgm, wgn, st, ##__VA_ARGS__>::LDS_USE, \
      ffn::TileCfg<bm, bn, bk, wgm, wgn, st, ##__VA_ARGS__>::NW,                                \
      ffn::TileCfg<bm, bn, bk, wgm, wgn, st, ##__VA_ARGS__>::WGK,                               \
+     ffn::TileCfg<bm, bn, bk, wgm, wgn, st, ##__VA_ARGS__>::PROD,                              \
      {ffn_launch_d0_v##id, ffn_launch_d1_v##id}},
 const Variant kVariants[] = {FFN_VARIANTS(FFN_VARIANT_ROW)};
 #undef FFN_VARIANT_ROW
@@ -94,12 +96,14 @@ constexpr double kUnitOverhead = 2.5e-6;   // s per unit: DMA prologue latency +
 // fragment reads per MFMA grow as the wave tile shrinks.  A K-sliced 128x128 tile has 128x64
 // wave tiles (and pays an LDS exchange of half its partials per tile); with eight waves, two
 // per SIMD, one wave's MFMAs cover the other's waits.  The K-sliced 64x64 tile (64x32 wave
-// tiles, two MFMAs per k-step) is a little ahead of the plain one.
+// tiles, two MFMAs per k-step) is a little ahead of the plain one.  A tile whose refill is
+// issued by waves of its own (no wave tile) keeps its tile waves off the texture unit: 1.6-8%
+// ahead of the same tile without them on the deep Basic downs.
 double tile_eff(const Variant& v) {
     const int a = v.bm < v.bn ? v.bm : v.bn, b = v.bm < v.bn ? v.bn : v.bm;
     if (v.wgk > 1) return a >= 128 ? (v.nw >= 8 ? 0.9 : 0.85) : 0.3;
     if (a >= 256) return 1.0;
-    if (a == 128 && b == 256) return 0.95;
+    if (a == 128 && b == 256) return v.prod > 0 ? 0.97 : 0.95;
     if (a == 128) return 0.6;
     if (a == 64 && b >= 128) return 0.42;
     return 0.25;
@@ -156,6 +160,7 @@ long long sk_grid(long long tiles, long long k_iters, int G) {
 constexpr size_t kCounterBytes = FFN_MI355X_WORKSPACE_COUNTER_BYTES;
 bool counters_fit(long long split_tiles, const Variant& v) { return split_tiles * v.nw * 4 <= (long long)kCounterBytes; }
 
+// (a tile with refill-only waves has no split form)
 bool sk_shape(const Variant& v, long long m_valid, long long N, long long K, int block_num, SkShape& s) {
     s.tiles = cdiv(m_valid, v.bm) * cdiv(N, v.bn);
     s.k_iters = cdiv(K, v.bk);
@@ -169,7 +174,7 @@ bool sk_shape(const Variant& v, long long m_valid, long long N, long long K, int
     const long long span = s.q + (s.r ? 1 : 0);
     // a range of `span` iterations touches at most ceil(span / k_iters) + 1 tiles
     s.slots = cdiv(span, s.k_iters) + 1;
-    return s.sk > 0 && s.k_iters >= 2 && counters_fit(s.sk, v);
+    return v.prod == 0 && s.sk > 0 && s.k_iters >= 2 && counters_fit(s.sk, v);
 }
 
 double cost_streamk(const Variant& v, const SkShape& s, long long m_valid, long long N, long long K) {
@@ -456,6 +461,10 @@ int ffn_mi355x_make_plan(int m, int mp, int kp, int hp, int np, int dtype, int d
     if (down_impl == FFN_MI355X_DOWN_STREAMK) {
         if (down_variant >= 0) {
             SkShape s;
+            if (kVariants[down_variant].prod > 0)
+                return fail(FFN_MI355X_ENOT_APPLICABLE,
+                            "tile variant %d runs whole tiles only (it has refill-only waves): no Stream-K form",
+                            down_variant);
             if (!sk_shape(kVariants[down_variant], m, np, hp, G, s)) {
                 if (s.k_iters < 2)
                     return fail(FFN_MI355X_ENOT_APPLICABLE,
@@ -791,6 +800,13 @@ int ffn_mi355x_run_noalloc(const ffn_mi355x_plan* plan, const void* x, const voi
 }
 
 int ffn_mi355x_num_variants(void) { return kNumVariants; }
+
+int ffn_mi355x_variant_refill_waves(int variant) {
+    if (variant < 0 || variant >= kNumVariants)
+        return fail(FFN_MI355X_EINVAL, "tile variant out of range (0..%d)", kNumVariants - 1);
+    ok();
+    return kVariants[variant].prod;
+}
 
 int ffn_mi355x_variant_info(int variant, int* bm, int* bn, int* bk, int* waves, int* stages,
                             int* lds_bytes) {

@@ -1,7 +1,7 @@
 // ffn_variants.hpp -- the macro-tile variants compiled into libffn_mi355x.so.
 //
 // X(id, BM, BN, BK, waves along M, waves along N, LDS stages[, sync slot, DMA k-steps,
-//   waves along K, waves issuing the refill])
+//   waves along K, waves issuing the refill, refill-only waves])
 // (DMA k-steps equal to the k-steps per stage spreads a deep pipeline's refill over the
 // whole iteration.)  The K-sliced 128x128 tiles (10, 11) give each wave a 128x64 wave tile
 // over half of every stage: a quarter fewer fragment reads per MFMA than 64x64 wave tiles,
@@ -13,6 +13,10 @@
 // Its refill goes out in the first k-step of the iteration (2% faster on the DiT-size up),
 // issued by waves 0-3 alone, one per SIMD (2-4% faster on the DiT-size GEMMs than all
 // eight waves sharing it).
+// Variant 17 is variant 1's tile with four more waves that only refill the LDS stages: each
+// SIMD pairs one refill wave with one tile wave that never waits on the texture unit (DiT-size
+// Basic down -1.6%, its 1536-deep shard -8%).  Such a tile runs whole tiles only: no Stream-K
+// or split form is built for it.
 // The deep-pipeline 64-row tiles (8, 9) keep 56 KiB or more of weights in flight per CU for
 // the memory-bound small-M (decode) shapes.  Variant 14 K-slices the 64x64 tile (64x32 wave
 // tiles over half of every stage): two MFMAs per k-step per wave instead of one, for the
@@ -42,9 +46,10 @@
     X(13, 128, 128, 64, 2, 2, 4, 3, 2, 2)   \
     X(14, 64, 64, 64, 1, 2, 6, -1, 2, 2)    \
     X(15, 32, 32, 128, 1, 1, 8, -1, 4, 2)   \
-    X(16, 64, 64, 128, 1, 2, 5, -1, 4, 2)
+    X(16, 64, 64, 128, 1, 2, 5, -1, 4, 2)   \
+    X(17, 256, 128, 64, 2, 2, 3, -1, 4, 1, 0, 4)
 
-#define FFN_NUM_VARIANTS 17
+#define FFN_NUM_VARIANTS 18
 
 
 // launch roles of one variant

@@ -149,6 +149,25 @@ def test_streamk_schedule_exact_once_and_slots(G):
             assert n.workspace_bytes == counters + Gs * n.down_slots_per_wg * n.down_bm * n.down_bn * 4
 
 
+def test_refill_wave_tiles_run_whole_tiles_only():
+    """A tile whose LDS refill is issued by waves of its own reports them (and counts them in its
+    waves), is never planned as a split up GEMM, and a forced Stream-K down on it is refused as
+    not applicable (no split form is built for it)."""
+    infos = _lib.variants()
+    refill = [v for v in infos if v["refill_waves"] > 0]
+    assert refill, "the DiT-size Basic down tile has refill-only waves"
+    for v in refill:
+        assert v["waves"] > v["refill_waves"]
+        with pytest.raises(NotApplicable, match="whole tiles only"):
+            _lib.make_plan(8192, 3072, 12288, 3072, _lib.BF16, "streamk", "erf", 256, -1, v["variant"])
+        for mp, kp, hp in [(64, 5120, 1728), (64, 1024, 4096)]:   # shapes other tiles split
+            n = _lib.make_plan(mp, kp, hp, 64, _lib.BF16, "basic", "erf", 256, v["variant"], -1)
+            assert n.up_sk_tiles == 0 and n.up_grid == min(n.up_tiles, 256)
+    assert all(v["refill_waves"] == 0 for v in infos if v not in refill)
+    with pytest.raises(ValueError):
+        _lib.check(_lib.load().ffn_mi355x_variant_refill_waves(len(infos)))
+
+
 @pytest.mark.parametrize("G", [8, 37, 256])
 def test_split_up_schedule_covers_once_and_shares_every_tile(G):
     """A split up GEMM (tiles filling at most half the grid, 16 or more K-iterations) covers
@@ -156,6 +175,7 @@ def test_split_up_schedule_covers_once_and_shares_every_tile(G):
     (its last piece applies the GELU), and its slots fit the workspace (brute force).
     Other up GEMMs keep one workgroup per tile."""
     lib = _lib.load()
+    refill = {v["variant"]: v["refill_waves"] for v in _lib.variants()}
     split_seen = 0
     for (mp, kp, hp) in [(64, 5120, 1728), (64, 1024, 4096), (320, 1008, 448), (128, 256, 1024),
                          (4096, 1024, 4096), (64, 5120, 13824)]:
@@ -164,7 +184,8 @@ def test_split_up_schedule_covers_once_and_shares_every_tile(G):
             kI, tiles = n.up_k_iters, n.up_tiles
             assert kI == -(-kp // n.up_bk)
             if n.up_sk_tiles == 0:
-                assert tiles * 2 > G or kI < 16
+                # (a tile with refill-only waves has no split form)
+                assert tiles * 2 > G or kI < 16 or refill[variant] > 0
                 assert n.up_grid == min(tiles, G)
                 continue
             split_seen += 1
@@ -549,12 +570,12 @@ def test_compile_kernel_binds_a_plan_without_a_device():
 # The tile each measured workload runs on, as the design notes' tile table states it:
 # (case id, down path) -> (up variant, down variant).
 TUNED_ASSIGNMENTS = {
-    ("c5_dit_bf16", "basic"): (12, 1), ("c5_dit_bf16", "streamk"): (12, 12),
+    ("c5_dit_bf16", "basic"): (12, 17), ("c5_dit_bf16", "streamk"): (12, 12),
     ("c2_aligned_bf16", "basic"): (12, 13), ("c2_aligned_bf16", "streamk"): (12, 1),
     ("c3_unaligned_fp16", "basic"): (13, 16), ("c3_unaligned_fp16", "streamk"): (13, 5),
     ("c4_decode_bf16", "basic"): (14, 15), ("c4_decode_bf16", "streamk"): (8, 14),
     ("c1_smoke_fp16", "basic"): (4, 15), ("c1_smoke_fp16", "streamk"): (4, 15),
-    ("c5_tp8_shard_bf16", "basic"): (12, 1), ("c5_tp8_shard_bf16", "streamk"): (12, 12),
+    ("c5_tp8_shard_bf16", "basic"): (12, 17), ("c5_tp8_shard_bf16", "streamk"): (12, 12),
     ("c4_tp8_shard_bf16", "basic"): (15, 15), ("c4_tp8_shard_bf16", "streamk"): (15, 16),
 }
 
