@@ -111,7 +111,7 @@ struct TileCfg {
     // issues MFMAs: while the first waits on the texture unit, the second keeps the matrix
     // core busy.
     static constexpr int DW = PROD > 0 ? PROD : DMAW_ == 0 ? NW : DMAW_;
-    static_assert(PROD == 0 || (WGK == 1 && DMAW_ == 0), "refill waves serve plain (not K-sliced) tiles");
+    static_assert(PROD == 0 || DMAW_ == 0, "refill-only waves issue the whole refill");
     static constexpr int A_PW = A_BLKS / DW, B_PW = B_BLKS / DW;  // DMA blocks per issuing wave
     static constexpr int LOADS = A_PW + B_PW;      // DMA instructions per issuing wave per stage
     static constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
@@ -413,6 +413,7 @@ struct Engine {
 
     lds_char* smem;
     int tid, lane, wave, wm, wn, wk;
+    int twave;  // index among the tile waves (0 for a refill-only wave)
     int a_row_off, b_row_off;  // per-lane LDS byte offsets of the fragment rows
     int swz;                   // chunk XOR of this lane's fragment rows
     static __device__ __forceinline__ int swz_of(int row) { return (row / C::R256) % C::CH; }
@@ -421,7 +422,8 @@ struct Engine {
         tid = threadIdx.x;
         lane = tid & 63;
         wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-        const int tw = MMA ? wave - C::PROD : 0;  // index among the tile waves
+        const int tw = MMA ? wave - C::PROD : 0;
+        twave = tw;
         wm = tw % C::WGM;
         wn = C::WGK == 1 ? tw / C::WGM : (tw / C::WGM) % C::WGN;
         wk = C::WGK == 1 ? 0 : tw / (C::WGM * C::WGN);
@@ -814,7 +816,6 @@ struct Engine {
     static constexpr int OSWZ = TPR < 16 ? TPR : 16;
     static constexpr int PIECES = ER * TPR / NT;         // pieces per thread per chunk
     static constexpr int PB = PIECES < 8 ? PIECES : 8;   // pieces in flight per thread
-    static_assert((ER * TPR) % NT == 0, "chunk pieces split evenly over the threads");
     static_assert(BPC >= 1 && FM % BPC == 0, "whole blocks per chunk");
 
     static __device__ __forceinline__ int out_off(int s, int ch) {
@@ -853,6 +854,7 @@ struct Engine {
     __device__ __forceinline__ void store_tile_lds_as(const GemmParams& p, const Unit& u, bool next,
                                                       f32x16 (&acc)[FN][FM]) {
         static_assert(C::OUT_POW2, "the staging swizzle needs a power-of-two number of pieces per row");
+        static_assert((ER * TPR) % NT == 0, "chunk pieces split evenly over the threads");
         lds_char* eb = smem + C::EPI_OFF;
         // DMA still in flight may target any stage but the next unit's prologue (issued last):
         // drain it; the barrier before the first staging write makes sure every wave has
@@ -1055,10 +1057,10 @@ struct Engine {
             constexpr int PK = 1 - WK;
             constexpr int nsend = FN * own_rows(PK), nrecv = FN * own_rows(WK);
             constexpr int b0 = PH * XB, b1 = (PH + 1) * XB;
-            const int partner = wave + (WK == 0 ? 1 : -1) * C::WGM * C::WGN;
+            const int partner = twave + (WK == 0 ? 1 : -1) * C::WGM * C::WGN;
             if constexpr (PH > 0) barrier();  // the partner has read the previous phase
             xsend<(own_rows(PK) > 0 ? own_rows(PK) : 1), own_base(PK), clampb(b0, nsend), clampb(b1, nsend)>(
-                smem + C::EPI_OFF + wave * XPW, acc);
+                smem + C::EPI_OFF + twave * XPW, acc);
             barrier();
             xrecv<(own_rows(WK) > 0 ? own_rows(WK) : 1), own_base(WK), clampb(b0, nrecv), clampb(b1, nrecv)>(
                 smem + C::EPI_OFF + partner * XPW, acc);
@@ -1075,6 +1077,22 @@ struct Engine {
         barrier();
         xphases<WK, 0>(acc);
         store_tile_regs<EPI, own_base(WK), own_base(WK) + own_rows(WK)>(p, u, acc);
+    }
+    // A refill-only wave's share of store_sliced: the same drain and the same barriers (one
+    // before the exchange, then those of xphases: two per phase but the first), no data.
+    template <int PH>
+    __device__ __forceinline__ void xphase_barriers() const {
+        if constexpr (PH * XB < XMAX) {
+            if constexpr (PH > 0) barrier();
+            barrier();
+            xphase_barriers<PH + 1>();
+        }
+    }
+    __device__ __forceinline__ void store_sliced_sync(bool next) const {
+        if (next) wait_vmcnt<C::LOADS * (S - 1)>();
+        else wait_vmcnt<0>();
+        barrier();
+        xphase_barriers<0>();
     }
     template <int EPI>
     __device__ __forceinline__ void store_sliced(const GemmParams& p, const Unit& u, bool next,
@@ -1234,8 +1252,9 @@ constexpr bool epi_in_regs() { return EPI != EPI_STORE || SK || !C::OUT_POW2 || 
 template <int DT, class C, int EPI, bool SK, bool FASTK, bool GATHER, bool ISSUE, bool MMA = true>
 __device__ __forceinline__ void walk_units(const GemmParams& p, lds_char* smem, int v, int G) {
     constexpr bool EPI_IN_REGS = epi_in_regs<C, EPI, SK>();
-    // the refill waves skip the epilogue, which therefore may hold no barrier
-    static_assert(C::PROD == 0 || (!SK && EPI_IN_REGS && C::WGK == 1), "refill waves: barrier-free epilogue only");
+    // the refill waves skip the epilogue's data: a register epilogue (no barrier) or a K-sliced
+    // tile's exchange, whose barriers they pass too; no split pieces
+    static_assert(C::PROD == 0 || (!SK && (EPI_IN_REGS || C::WGK > 1)), "refill waves: whole tiles only");
     Engine<DT, C, GATHER, ISSUE, MMA> eng(smem, p);
     f32x16 acc[C::FN][C::FM];
     UnitWalker<SK> walk(p, v, G);
@@ -1256,6 +1275,8 @@ __device__ __forceinline__ void walk_units(const GemmParams& p, lds_char* smem, 
                 eng.template store_tile_regs<EPI>(p, u, acc);
             else
                 eng.template store_tile_lds<EPI>(p, u, nx.valid, acc);
+        } else if constexpr (C::WGK > 1) {
+            eng.store_sliced_sync(nx.valid);
         }
         if (!nx.valid) break;
         u = nx;

@@ -97,16 +97,17 @@ constexpr double kUnitOverhead = 2.5e-6;   // s per unit: DMA prologue latency +
 // wave tiles (and pays an LDS exchange of half its partials per tile); with eight waves, two
 // per SIMD, one wave's MFMAs cover the other's waits.  The K-sliced 64x64 tile (64x32 wave
 // tiles, two MFMAs per k-step) is a little ahead of the plain one.  A tile whose refill is
-// issued by waves of its own (no wave tile) keeps its tile waves off the texture unit: 1.6-8%
-// ahead of the same tile without them on the deep Basic downs.
+// issued by waves of its own (no wave tile) keeps its tile waves off the texture unit: 1.6-18%
+// ahead of the same tile without them on the Basic downs and unaligned up it serves.
 double tile_eff(const Variant& v) {
     const int a = v.bm < v.bn ? v.bm : v.bn, b = v.bm < v.bn ? v.bn : v.bm;
-    if (v.wgk > 1) return a >= 128 ? (v.nw >= 8 ? 0.9 : 0.85) : 0.3;
-    if (a >= 256) return 1.0;
-    if (a == 128 && b == 256) return v.prod > 0 ? 0.97 : 0.95;
-    if (a == 128) return 0.6;
-    if (a == 64 && b >= 128) return 0.42;
-    return 0.25;
+    const double refill = v.prod > 0 ? 1.03 : 1.0;
+    if (v.wgk > 1) return refill * (a >= 128 ? (v.nw >= 8 ? 0.9 : 0.85) : 0.3);
+    if (a >= 256) return refill * 1.0;
+    if (a == 128 && b == 256) return refill * 0.95;
+    if (a == 128) return refill * 0.6;
+    if (a == 64 && b >= 128) return refill * 0.42;
+    return refill * 0.25;
 }
 
 // Seconds per BK-deep iteration of one workgroup on a tile with `rows` data-bearing rows.

@@ -448,20 +448,25 @@ def _k_sliced_variants():
 
 
 def test_k_sliced_variants_plan_for_basic_and_streamk():
-    """The K-sliced tiles (two waves along K) report two, four or eight waves, are planned for
-    the up GEMM and the Basic down, and have a Stream-K form (the slices are summed before a
-    split piece writes its partial)."""
+    """The K-sliced tiles (two waves along K) report two, four or eight tile waves (plus their
+    refill-only waves, if any), are planned for the up GEMM and the Basic down, and have a
+    Stream-K form (the slices are summed before a split piece writes its partial) unless they
+    have refill-only waves."""
     from ffn_optim_amd import _lib
     ids = _k_sliced_variants()
-    assert {10, 11, 13, 14, 15, 16} == ids
+    assert {10, 11, 13, 14, 15, 16, 18, 19, 20} == ids
     sliced = [v for v in _lib.variants() if v["variant"] in ids]
     for v in sliced:
-        assert v["waves"] in (2, 4, 8) and v["lds_bytes"] <= 160 * 1024
+        assert v["waves"] - v["refill_waves"] in (2, 4, 8) and v["lds_bytes"] <= 160 * 1024
         plan = _lib.make_plan(4096, 1024, 4096, 1024, _lib.BF16, "basic", "erf", 256,
                               v["variant"], v["variant"])
         assert (plan.up_variant, plan.down_variant) == (v["variant"], v["variant"])
         assert plan.workspace_bytes == 0
         # decode down: 16 rows, 5120 wide, 13824 deep -- every tile count leaves a remainder
+        if v["refill_waves"]:
+            with pytest.raises(NotApplicable):
+                _lib.make_plan(64, 5120, 13824, 5120, _lib.BF16, "streamk", "erf", 256, 8, v["variant"], m=16)
+            continue
         plan = _lib.make_plan(64, 5120, 13824, 5120, _lib.BF16, "streamk", "erf", 256, 8, v["variant"], m=16)
         assert plan.down_variant == v["variant"] and plan.down_sk_tiles > 0 and plan.workspace_bytes > 0
 
@@ -572,11 +577,11 @@ def test_compile_kernel_binds_a_plan_without_a_device():
 TUNED_ASSIGNMENTS = {
     ("c5_dit_bf16", "basic"): (12, 17), ("c5_dit_bf16", "streamk"): (12, 12),
     ("c2_aligned_bf16", "basic"): (12, 13), ("c2_aligned_bf16", "streamk"): (12, 1),
-    ("c3_unaligned_fp16", "basic"): (13, 16), ("c3_unaligned_fp16", "streamk"): (13, 5),
-    ("c4_decode_bf16", "basic"): (14, 15), ("c4_decode_bf16", "streamk"): (8, 14),
-    ("c1_smoke_fp16", "basic"): (4, 15), ("c1_smoke_fp16", "streamk"): (4, 15),
+    ("c3_unaligned_fp16", "basic"): (18, 19), ("c3_unaligned_fp16", "streamk"): (18, 5),
+    ("c4_decode_bf16", "basic"): (8, 20), ("c4_decode_bf16", "streamk"): (8, 14),
+    ("c1_smoke_fp16", "basic"): (4, 20), ("c1_smoke_fp16", "streamk"): (4, 15),
     ("c5_tp8_shard_bf16", "basic"): (12, 17), ("c5_tp8_shard_bf16", "streamk"): (12, 12),
-    ("c4_tp8_shard_bf16", "basic"): (15, 15), ("c4_tp8_shard_bf16", "streamk"): (15, 16),
+    ("c4_tp8_shard_bf16", "basic"): (15, 20), ("c4_tp8_shard_bf16", "streamk"): (15, 16),
 }
 
 
