@@ -1104,15 +1104,16 @@ struct Engine {
 
     // FP32 partial tile in the accumulator's own register order: group (j, i, q) of logical
     // thread t lives at ((j*FM + i)*4 + q)*NTL + t (16-byte units), so every store is coalesced.
-    // t is the thread's index among the WGM x WGN waves of one K slice, NTL their thread count:
-    // a K-sliced tile first sums its slices (the exchange above) and each slice then writes the
-    // row blocks [I0, I1) it owns.
-    static constexpr int NTL = C::NT / C::WGK;
+    // t is the thread's index among the WGM x WGN tile waves of one K slice, NTL their thread
+    // count: a K-sliced tile first sums its slices (the exchange above) and each slice then
+    // writes the row blocks [I0, I1) it owns.  (Refill-only waves, numbered first, hold none.)
+    static constexpr int NTL = C::NW * 64 / C::WGK;
+    __device__ __forceinline__ int slice_thread() const { return tid - C::PROD * 64 - wk * NTL; }
     static __device__ __forceinline__ uint32_t part_off(int idx, int t) { return (uint32_t)(idx * NTL + t) * 16u; }
     template <int I0 = 0, int I1 = FM>
     __device__ __forceinline__ void store_partial(const __amdgpu_buffer_rsrc_t& r, uint32_t slot_off,
                                                   f32x16 (&acc)[FN][FM]) const {
-        const int t = tid - wk * NTL;
+        const int t = slice_thread();
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
@@ -1171,13 +1172,13 @@ struct Engine {
         const int kI = p.k_iters, sp = u.split;
         const int first = sk_owner(p, sp * kI), last = sk_owner(p, sp * kI + kI - 1);
         wait_vmcnt<0>();
-        unsigned* flag = p.sk_flags + (size_t)sp * C::NW + wave;
+        unsigned* flag = p.sk_flags + (size_t)sp * C::NW + twave;
         unsigned old = 0;
         if (lane == 0) old = __hip_atomic_fetch_add(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         old = (unsigned)__builtin_amdgcn_readfirstlane((int)old);
         if (old != (unsigned)(last - first)) return;
         if (lane == 0) __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int t = tid - wk * NTL;
+        const int t = slice_thread();
         auto slot_of = [&](int w) {
             return (uint32_t)((sk_slot(p, w, sp - sk_start(p, w) / kI, C::BM * C::BN) - p.ws) * 4);
         };
@@ -1252,9 +1253,9 @@ constexpr bool epi_in_regs() { return EPI != EPI_STORE || SK || !C::OUT_POW2 || 
 template <int DT, class C, int EPI, bool SK, bool FASTK, bool GATHER, bool ISSUE, bool MMA = true>
 __device__ __forceinline__ void walk_units(const GemmParams& p, lds_char* smem, int v, int G) {
     constexpr bool EPI_IN_REGS = epi_in_regs<C, EPI, SK>();
-    // the refill waves skip the epilogue's data: a register epilogue (no barrier) or a K-sliced
-    // tile's exchange, whose barriers they pass too; no split pieces
-    static_assert(C::PROD == 0 || (!SK && (EPI_IN_REGS || C::WGK > 1)), "refill waves: whole tiles only");
+    // the refill waves skip the epilogue's data: a register epilogue or a split piece's partial
+    // and finish (no barrier), or a K-sliced tile's exchange, whose barriers they pass too
+    static_assert(C::PROD == 0 || EPI_IN_REGS || C::WGK > 1, "refill waves: no staged epilogue");
     Engine<DT, C, GATHER, ISSUE, MMA> eng(smem, p);
     f32x16 acc[C::FN][C::FM];
     UnitWalker<SK> walk(p, v, G);

@@ -47,12 +47,6 @@ template <class CFG>
 hipError_t launch_role(int role, const ffn::GemmParams* p, int grid, hipStream_t stream) {
     using namespace ffn;
     const dim3 g(grid), b(CFG::NT);
-    if constexpr (CFG::PROD > 0) {
-        // a tile with refill waves runs whole tiles only (no split pieces)
-        if (role == FFN_ROLE_DOWN_STREAMK || role == FFN_ROLE_UP_SPLIT_ERF || role == FFN_ROLE_UP_SPLIT_RATIONAL ||
-            role == FFN_ROLE_UP_SPLIT_SILU)
-            return hipErrorInvalidValue;
-    }
     switch (role) {
         case FFN_ROLE_UP_ERF:
             launch_gemm<CFG, EPI_GELU_ERF, false>(p, g, b, stream);
@@ -64,13 +58,13 @@ hipError_t launch_role(int role, const ffn::GemmParams* p, int grid, hipStream_t
             launch_gemm<CFG, EPI_STORE, false>(p, g, b, stream);
             break;
         case FFN_ROLE_DOWN_STREAMK:
-            if constexpr (CFG::PROD == 0) launch_gemm<CFG, EPI_STORE, true>(p, g, b, stream);
+            launch_gemm<CFG, EPI_STORE, true>(p, g, b, stream);
             break;
         case FFN_ROLE_UP_SPLIT_ERF:
-            if constexpr (CFG::PROD == 0) launch_gemm<CFG, EPI_GELU_ERF, true>(p, g, b, stream);
+            launch_gemm<CFG, EPI_GELU_ERF, true>(p, g, b, stream);
             break;
         case FFN_ROLE_UP_SPLIT_RATIONAL:
-            if constexpr (CFG::PROD == 0) launch_gemm<CFG, EPI_GELU_RATIONAL, true>(p, g, b, stream);
+            launch_gemm<CFG, EPI_GELU_RATIONAL, true>(p, g, b, stream);
             break;
         case FFN_ROLE_UP_SILU:
             launch_gemm<CFG, EPI_SILU, false>(p, g, b, stream);
@@ -80,7 +74,7 @@ hipError_t launch_role(int role, const ffn::GemmParams* p, int grid, hipStream_t
             else return hipErrorInvalidValue;
             break;
         case FFN_ROLE_UP_SPLIT_SILU:
-            if constexpr (CFG::PROD == 0) launch_gemm<CFG, EPI_SILU, true>(p, g, b, stream);
+            launch_gemm<CFG, EPI_SILU, true>(p, g, b, stream);
             break;
         default:
             return hipErrorInvalidValue;

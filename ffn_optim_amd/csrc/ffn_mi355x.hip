@@ -43,7 +43,7 @@ struct Variant {
     int lds_bytes;            // LDS of one workgroup: the stages plus any epilogue staging beyond
     int nw;                   // waves holding wave tiles
     int wgk;                  // waves along K (K-sliced tile when > 1)
-    int prod;                 // waves that only refill the LDS stages (whole tiles only when > 0)
+    int prod;                 // waves that only refill the LDS stages
     ffn_launch_fn launch[2];  // [dtype]
     int waves() const { return nw + prod; }
     int lds() const { return lds_bytes; }
@@ -161,7 +161,6 @@ long long sk_grid(long long tiles, long long k_iters, int G) {
 constexpr size_t kCounterBytes = FFN_MI355X_WORKSPACE_COUNTER_BYTES;
 bool counters_fit(long long split_tiles, const Variant& v) { return split_tiles * v.nw * 4 <= (long long)kCounterBytes; }
 
-// (a tile with refill-only waves has no split form)
 bool sk_shape(const Variant& v, long long m_valid, long long N, long long K, int block_num, SkShape& s) {
     s.tiles = cdiv(m_valid, v.bm) * cdiv(N, v.bn);
     s.k_iters = cdiv(K, v.bk);
@@ -175,7 +174,7 @@ bool sk_shape(const Variant& v, long long m_valid, long long N, long long K, int
     const long long span = s.q + (s.r ? 1 : 0);
     // a range of `span` iterations touches at most ceil(span / k_iters) + 1 tiles
     s.slots = cdiv(span, s.k_iters) + 1;
-    return v.prod == 0 && s.sk > 0 && s.k_iters >= 2 && counters_fit(s.sk, v);
+    return s.sk > 0 && s.k_iters >= 2 && counters_fit(s.sk, v);
 }
 
 double cost_streamk(const Variant& v, const SkShape& s, long long m_valid, long long N, long long K) {
@@ -462,10 +461,6 @@ int ffn_mi355x_make_plan(int m, int mp, int kp, int hp, int np, int dtype, int d
     if (down_impl == FFN_MI355X_DOWN_STREAMK) {
         if (down_variant >= 0) {
             SkShape s;
-            if (kVariants[down_variant].prod > 0)
-                return fail(FFN_MI355X_ENOT_APPLICABLE,
-                            "tile variant %d runs whole tiles only (it has refill-only waves): no Stream-K form",
-                            down_variant);
             if (!sk_shape(kVariants[down_variant], m, np, hp, G, s)) {
                 if (s.k_iters < 2)
                     return fail(FFN_MI355X_ENOT_APPLICABLE,

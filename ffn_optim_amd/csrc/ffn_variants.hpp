@@ -18,8 +18,7 @@
 // wait on the texture unit.  DiT-size Basic down -1.6% (17), its 1536-deep shard -8%; unaligned
 // up -4% (18) and Basic down -8.5% (19); decode Basic down -18% (20) while its weights stay in
 // the last-level cache (smoke and decode-shard FFNs; the full decode FFN streams them from HBM
-// at the same rate either way).  Such a tile runs whole tiles only: no Stream-K or split form
-// is built for it.
+// at the same rate either way).
 // The deep-pipeline 64-row tiles (8, 9) keep 56 KiB or more of weights in flight per CU for
 // the memory-bound small-M (decode) shapes.  Variant 14 K-slices the 64x64 tile (64x32 wave
 // tiles over half of every stage): two MFMAs per k-step per wave instead of one, for the

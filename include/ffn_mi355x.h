@@ -209,8 +209,7 @@ int ffn_mi355x_variant_info(int variant, int* bm, int* bn, int* bk, int* waves, 
                             int* lds_bytes);
 
 /* Waves of a tile variant that only refill its LDS stages (0 for most tiles; `waves` above
- * counts them too), or a negative code for a variant out of range.  Such a tile runs whole
- * tiles only: a Stream-K down or a split up GEMM is not planned on it.  No counterpart in the
+ * counts them too), or a negative code for a variant out of range.  No counterpart in the
  * reference, whose tiles are fixed (ops/host/tiling.py:11-25): it describes this build's
  * tile table for planners and tests. */
 int ffn_mi355x_variant_refill_waves(int variant);

@@ -149,20 +149,18 @@ def test_streamk_schedule_exact_once_and_slots(G):
             assert n.workspace_bytes == counters + Gs * n.down_slots_per_wg * n.down_bm * n.down_bn * 4
 
 
-def test_refill_wave_tiles_run_whole_tiles_only():
-    """A tile whose LDS refill is issued by waves of its own reports them (and counts them in its
-    waves), is never planned as a split up GEMM, and a forced Stream-K down on it is refused as
-    not applicable (no split form is built for it)."""
+def test_refill_wave_tiles_report_their_waves():
+    """Tiles whose LDS refill is issued by waves of their own report them and count them in
+    their waves; they plan like every other tile (whole, Stream-K and split up GEMMs), and the
+    query refuses an out-of-range variant."""
     infos = _lib.variants()
     refill = [v for v in infos if v["refill_waves"] > 0]
-    assert refill, "the DiT-size Basic down tile has refill-only waves"
+    assert {v["variant"] for v in refill} == {17, 18, 19, 20}
     for v in refill:
-        assert v["waves"] > v["refill_waves"]
-        with pytest.raises(NotApplicable, match="whole tiles only"):
-            _lib.make_plan(8192, 3072, 12288, 3072, _lib.BF16, "streamk", "erf", 256, -1, v["variant"])
-        for mp, kp, hp in [(64, 5120, 1728), (64, 1024, 4096)]:   # shapes other tiles split
-            n = _lib.make_plan(mp, kp, hp, 64, _lib.BF16, "basic", "erf", 256, v["variant"], -1)
-            assert n.up_sk_tiles == 0 and n.up_grid == min(n.up_tiles, 256)
+        assert v["waves"] > v["refill_waves"] > 0
+        # decode down: 16 rows, 5120 wide, 13824 deep -- every tile count leaves a remainder
+        plan = _lib.make_plan(64, 5120, 13824, 5120, _lib.BF16, "streamk", "erf", 256, 8, v["variant"], m=16)
+        assert plan.down_variant == v["variant"] and plan.down_sk_tiles > 0
     assert all(v["refill_waves"] == 0 for v in infos if v not in refill)
     with pytest.raises(ValueError):
         _lib.check(_lib.load().ffn_mi355x_variant_refill_waves(len(infos)))
@@ -175,7 +173,6 @@ def test_split_up_schedule_covers_once_and_shares_every_tile(G):
     (its last piece applies the GELU), and its slots fit the workspace (brute force).
     Other up GEMMs keep one workgroup per tile."""
     lib = _lib.load()
-    refill = {v["variant"]: v["refill_waves"] for v in _lib.variants()}
     split_seen = 0
     for (mp, kp, hp) in [(64, 5120, 1728), (64, 1024, 4096), (320, 1008, 448), (128, 256, 1024),
                          (4096, 1024, 4096), (64, 5120, 13824)]:
@@ -184,8 +181,7 @@ def test_split_up_schedule_covers_once_and_shares_every_tile(G):
             kI, tiles = n.up_k_iters, n.up_tiles
             assert kI == -(-kp // n.up_bk)
             if n.up_sk_tiles == 0:
-                # (a tile with refill-only waves has no split form)
-                assert tiles * 2 > G or kI < 16 or refill[variant] > 0
+                assert tiles * 2 > G or kI < 16
                 assert n.up_grid == min(tiles, G)
                 continue
             split_seen += 1
@@ -450,8 +446,7 @@ def _k_sliced_variants():
 def test_k_sliced_variants_plan_for_basic_and_streamk():
     """The K-sliced tiles (two waves along K) report two, four or eight tile waves (plus their
     refill-only waves, if any), are planned for the up GEMM and the Basic down, and have a
-    Stream-K form (the slices are summed before a split piece writes its partial) unless they
-    have refill-only waves."""
+    Stream-K form (the slices are summed before a split piece writes its partial)."""
     from ffn_optim_amd import _lib
     ids = _k_sliced_variants()
     assert {10, 11, 13, 14, 15, 16, 18, 19, 20} == ids
@@ -463,10 +458,6 @@ def test_k_sliced_variants_plan_for_basic_and_streamk():
         assert (plan.up_variant, plan.down_variant) == (v["variant"], v["variant"])
         assert plan.workspace_bytes == 0
         # decode down: 16 rows, 5120 wide, 13824 deep -- every tile count leaves a remainder
-        if v["refill_waves"]:
-            with pytest.raises(NotApplicable):
-                _lib.make_plan(64, 5120, 13824, 5120, _lib.BF16, "streamk", "erf", 256, 8, v["variant"], m=16)
-            continue
         plan = _lib.make_plan(64, 5120, 13824, 5120, _lib.BF16, "streamk", "erf", 256, 8, v["variant"], m=16)
         assert plan.down_variant == v["variant"] and plan.down_sk_tiles > 0 and plan.workspace_bytes > 0
 
@@ -576,12 +567,12 @@ def test_compile_kernel_binds_a_plan_without_a_device():
 # (case id, down path) -> (up variant, down variant).
 TUNED_ASSIGNMENTS = {
     ("c5_dit_bf16", "basic"): (12, 17), ("c5_dit_bf16", "streamk"): (12, 12),
-    ("c2_aligned_bf16", "basic"): (12, 13), ("c2_aligned_bf16", "streamk"): (12, 1),
+    ("c2_aligned_bf16", "basic"): (12, 13), ("c2_aligned_bf16", "streamk"): (12, 17),
     ("c3_unaligned_fp16", "basic"): (18, 19), ("c3_unaligned_fp16", "streamk"): (18, 5),
-    ("c4_decode_bf16", "basic"): (8, 20), ("c4_decode_bf16", "streamk"): (8, 14),
-    ("c1_smoke_fp16", "basic"): (4, 20), ("c1_smoke_fp16", "streamk"): (4, 15),
+    ("c4_decode_bf16", "basic"): (8, 20), ("c4_decode_bf16", "streamk"): (8, 19),
+    ("c1_smoke_fp16", "basic"): (4, 20), ("c1_smoke_fp16", "streamk"): (4, 20),
     ("c5_tp8_shard_bf16", "basic"): (12, 17), ("c5_tp8_shard_bf16", "streamk"): (12, 12),
-    ("c4_tp8_shard_bf16", "basic"): (15, 20), ("c4_tp8_shard_bf16", "streamk"): (15, 16),
+    ("c4_tp8_shard_bf16", "basic"): (15, 20), ("c4_tp8_shard_bf16", "streamk"): (19, 19),
 }
 
 
