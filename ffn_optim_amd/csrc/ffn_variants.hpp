@@ -13,10 +13,12 @@
 // Its refill goes out in the first k-step of the iteration (2% faster on the DiT-size up),
 // issued by waves 0-3 alone, one per SIMD (2-4% faster on the DiT-size GEMMs than all
 // eight waves sharing it).
-// Variants 17-20 are variants 1, 13, 16 and 15 with more waves that only refill the LDS stages
-// (four; two for the two-wave 15): each SIMD holds refill waves beside tile waves that never
-// wait on the texture unit.  DiT-size Basic down -1.6% (17), its 1536-deep shard -8%; unaligned
-// up -4% (18) and Basic down -8.5% (19); decode Basic down -18% (20) while its weights stay in
+// Variants 17-21 are variants 1, 13, 16, 15 and 11 with more waves that only refill the LDS
+// stages (four; two for the two-wave 15): each SIMD holds refill waves beside tile waves that
+// never wait on the texture unit.  DiT-size Basic down -1.6% (17), its 1536-deep shard -8%;
+// unaligned up -4% (18) and Basic down -8.5% (19); aligned mid-size Basic down -3 to -6% (21,
+// whose 128x64 wave tiles read less LDS per MFMA than variant 13's 64x64, with two waves per
+// SIMD now); decode Basic down -18% (20) while its weights stay in
 // the last-level cache (smoke and decode-shard FFNs; the full decode FFN streams them from HBM
 // at the same rate either way).
 // The deep-pipeline 64-row tiles (8, 9) keep 56 KiB or more of weights in flight per CU for
@@ -52,9 +54,10 @@
     X(17, 256, 128, 64, 2, 2, 3, -1, 4, 1, 0, 4) \
     X(18, 128, 128, 64, 2, 2, 4, 3, 2, 2, 0, 4)  \
     X(19, 64, 64, 128, 1, 2, 5, -1, 4, 2, 0, 4)  \
-    X(20, 32, 32, 128, 1, 1, 8, -1, 4, 2, 0, 2)
+    X(20, 32, 32, 128, 1, 1, 8, -1, 4, 2, 0, 2)  \
+    X(21, 128, 128, 64, 1, 2, 4, -1, 2, 2, 0, 4)
 
-#define FFN_NUM_VARIANTS 21
+#define FFN_NUM_VARIANTS 22
 
 
 // launch roles of one variant

@@ -155,7 +155,7 @@ def test_refill_wave_tiles_report_their_waves():
     query refuses an out-of-range variant."""
     infos = _lib.variants()
     refill = [v for v in infos if v["refill_waves"] > 0]
-    assert {v["variant"] for v in refill} == {17, 18, 19, 20}
+    assert {v["variant"] for v in refill} == {17, 18, 19, 20, 21}
     for v in refill:
         assert v["waves"] > v["refill_waves"] > 0
         # decode down: 16 rows, 5120 wide, 13824 deep -- every tile count leaves a remainder
@@ -449,7 +449,7 @@ def test_k_sliced_variants_plan_for_basic_and_streamk():
     Stream-K form (the slices are summed before a split piece writes its partial)."""
     from ffn_optim_amd import _lib
     ids = _k_sliced_variants()
-    assert {10, 11, 13, 14, 15, 16, 18, 19, 20} == ids
+    assert {10, 11, 13, 14, 15, 16, 18, 19, 20, 21} == ids
     sliced = [v for v in _lib.variants() if v["variant"] in ids]
     for v in sliced:
         assert v["waves"] - v["refill_waves"] in (2, 4, 8) and v["lds_bytes"] <= 160 * 1024
@@ -567,7 +567,7 @@ def test_compile_kernel_binds_a_plan_without_a_device():
 # (case id, down path) -> (up variant, down variant).
 TUNED_ASSIGNMENTS = {
     ("c5_dit_bf16", "basic"): (12, 17), ("c5_dit_bf16", "streamk"): (12, 12),
-    ("c2_aligned_bf16", "basic"): (12, 13), ("c2_aligned_bf16", "streamk"): (12, 17),
+    ("c2_aligned_bf16", "basic"): (12, 21), ("c2_aligned_bf16", "streamk"): (12, 17),
     ("c3_unaligned_fp16", "basic"): (18, 19), ("c3_unaligned_fp16", "streamk"): (18, 5),
     ("c4_decode_bf16", "basic"): (8, 20), ("c4_decode_bf16", "streamk"): (8, 19),
     ("c1_smoke_fp16", "basic"): (4, 20), ("c1_smoke_fp16", "streamk"): (4, 20),
