@@ -1244,7 +1244,7 @@ struct Engine {
 // A K-sliced tile exchanges its partial sums through the free stage(s) and stores from
 // registers; its Stream-K pieces exchange first and then store their FP32 partials.  A tile
 // whose output rows are not a power-of-two number of 16-byte pieces stores from registers, and
-// so does a tile with refill waves (which hold no output).
+// so does a tile with refill-only waves: they skip the epilogue, which may then hold no barrier.
 template <class C, int EPI, bool SK>
 constexpr bool epi_in_regs() { return EPI != EPI_STORE || SK || !C::OUT_POW2 || C::PROD > 0; }
 
