@@ -410,6 +410,49 @@ def test_every_variant_at_logical_widths(dtype):
         assert res["passed"], (v, res)
 
 
+def _refill_bases():
+    """(refill-wave tile, its base tile): same macro tile, stages and tile waves, no refill
+    waves (the base's waves equal the tile waves of the other)."""
+    infos = _lib.variants()
+    pairs = []
+    for v in infos:
+        if v["refill_waves"] == 0:
+            continue
+        base = [b for b in infos if b["refill_waves"] == 0 and b["waves"] == v["waves"] - v["refill_waves"]
+                and all(b[f] == v[f] for f in ("bm", "bn", "bk", "stages"))]
+        assert base, v
+        pairs.append((v["variant"], base[0]["variant"]))
+    return pairs
+
+
+@pytest.mark.parametrize("down", ["basic", "streamk"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_refill_wave_tiles_match_their_base_tiles(dtype, down):
+    """A tile whose refill is issued by waves of its own computes exactly what its base tile
+    computes (same MFMAs in the same order): whole FFNs, forced on both GEMMs, on ragged widths
+    (K and H tails, partial tiles), Basic and Stream-K, are bit-identical."""
+    g = torch.Generator().manual_seed(45)
+    m, k, h, n = 300, 1000, 1400, 264
+    x = torch.randn(m, k, generator=g).to(dtype).cuda()
+    w1 = (torch.randn(h, k, generator=g) * k ** -0.5).to(dtype).cuda()
+    w2 = (torch.randn(n, h, generator=g) * h ** -0.5).to(dtype).cuda()
+    pairs = _refill_bases()
+    assert len(pairs) >= 5
+    ran = 0
+    for v, b in pairs:
+        try:
+            got = prepare_ffn(x, w1, w2, down_impl=down, up_variant=v, down_variant=v)
+            ref = prepare_ffn(x, w1, w2, down_impl=down, up_variant=b, down_variant=b)
+        except ValueError:       # Stream-K not applicable to this tile count
+            continue
+        say("refill vs base", dtype, down, v, b, got.plan.native.up_sk_tiles, got.plan.native.down_sk_tiles)
+        y, r = got.run(), ref.run()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), r.view(torch.int16)), (v, b, down)
+        ran += 1
+    assert ran >= 3
+
+
 def test_buffers_outside_their_allocation_are_refused():
     """The C ABI checks every buffer's span against its device allocation before launching:
     a host pointer or a buffer shorter than the plan needs returns an error, nothing runs."""
