@@ -1,8 +1,8 @@
 """FP32 golden and the error criterion the harness validates candidates with.
 
 golden() composes torch CPU FP32 ops in the order of validation/reference.py:16-23
-(X reshaped to [m, k] @ W1^T -> exact or rational GELU -> @ W2^T -> cast to the input
-dtype -> leading dims restored); compare() is validation/test_ffn.py:6-21:
+(X reshaped to [m, k] @ W1^T -> exact or rational GELU -> [staged: cast to the input dtype and
+back] -> @ W2^T -> cast to the input dtype -> leading dims restored); compare() is validation/test_ffn.py:6-21:
 shape/dtype/finiteness, max_abs, rms and mean(|a-b|/(|b|+1e-3)) < 0.05.
 """
 from __future__ import annotations
@@ -29,13 +29,17 @@ def gelu_rational(x):
     return x * 0.5 * (p / q + 1.0)
 
 
-def golden(x, w1, w2, gelu="erf"):
-    """CPU FP32 reference output in the input dtype."""
+def golden(x, w1, w2, gelu="erf", staged=False):
+    """CPU FP32 reference output in the input dtype.  staged rounds the hidden activation to the
+    input dtype before the second product, as the kernels store it (the reference's staged
+    golden, validation/reference.py:16-23)."""
     import torch
     m, k = x.numel() // x.shape[-1], x.shape[-1]
     xs = x.detach().cpu().reshape(m, k).float()
     z = xs @ w1.detach().cpu().float().T
     h = torch.nn.functional.gelu(z, approximate="none") if gelu == "erf" else gelu_rational(z)
+    if staged:
+        h = h.to(x.dtype).float()
     y = h @ w2.detach().cpu().float().T
     return y.to(x.dtype).reshape(*x.shape[:-1], w2.shape[0])
 

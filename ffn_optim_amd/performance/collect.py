@@ -17,31 +17,36 @@ from pathlib import Path
 FFN_KERNEL = "ffn_"   # kernel-name fragment of every FFN kernel (ffn_gemm_kernel)
 
 
+def _event_us(fn):
+    """Device time of one fn() call on the current stream, in microseconds: an event pair around
+    the call, waited for before returning (so calls never queue up behind each other)."""
+    import torch
+    pair = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    pair[0].record()
+    fn()
+    pair[1].record()
+    pair[1].synchronize()
+    return pair[0].elapsed_time(pair[1]) * 1000.0
+
+
 def time_prepared(prepared, warmup=5, repeats=20, *, progress=None):
-    """Warm up, then time each of `repeats` run() calls with its own event pair on the
-    preparation stream (performance/collect.py:8-35).  Returns device_median_us and the
-    samples; a non-finite or non-positive sample rejects the candidate."""
+    """The harness's ranking time of one PreparedFFN: `warmup` untimed run() calls, then
+    `repeats` calls with an event pair each; the median in microseconds (the protocol of
+    performance/collect.py:8-35).  Returns device_median_us with the samples; a non-finite or
+    non-positive sample refuses the candidate (RuntimeError)."""
     if warmup < 0 or repeats < 1:
         raise ValueError("warmup >= 0 and repeats >= 1 required")
     import torch
+    say = progress or (lambda message: None)
     device = prepared.storage[0].device
     with torch.cuda.device(device):
-        if progress is not None:
-            progress(f"device warm-up: {warmup} runs")
+        say(f"device warm-up: {warmup} runs")
         for _ in range(warmup):
             prepared.run()
         torch.cuda.synchronize(device)
-        if progress is not None:
-            progress(f"warm-up done, timing {repeats} runs")
-        samples = []
-        for _ in range(repeats):
-            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            start.record()
-            prepared.run()
-            end.record()
-            end.synchronize()
-            samples.append(start.elapsed_time(end) * 1000)
-    if any(not math.isfinite(s) or s <= 0 for s in samples):
+        say(f"warm-up done, timing {repeats} runs")
+        samples = [_event_us(prepared.run) for _ in range(repeats)]
+    if not all(math.isfinite(v) and v > 0 for v in samples):
         raise RuntimeError("Invalid device timing; refusing to rank this candidate")
     return {"device_median_us": statistics.median(samples), "device_samples_us": samples,
             "warmup": warmup, "repeats": repeats, "task_duration_us": None,

@@ -1,24 +1,95 @@
-"""Serial exhaustive search over an explicit candidate list (restates performance/tune.py).
+"""Candidate spaces and ranking of the measurement harness (the counterpart of performance/tune.py).
 
-combinations() builds the reference's implementation Cartesian product;
-tile_space_up()/tile_space_down() add the MI355X-specific dimension, the tile variants
-the library accepts for a problem, searched one GEMM at a time.  search() evaluates candidates in order, checkpoints after each
-one and ranks only candidates whose status is 'passed' with a finite positive
-unprofiled device-event median.  refine_candidates() picks the near-equal finalists that tune
-mode re-times side by side, and pick_fastest() ranks by that re-timing where it exists.
+A harness run evaluates candidates one at a time; each evaluation returns a record whose
+``status`` says how far it got (planned, unavailable, not_applicable, compile_failed,
+accuracy_failed, passed, ...).  Only a ``passed`` record with a finite, positive unprofiled
+device-event median (``device_median_us``) can become a case's best: the ``Leaderboard`` below
+keeps that rule in one place.
+
+Candidate spaces:
+* ``combinations`` -- the implementation product the reference searches (up x down impls);
+* ``tile_space_up`` / ``tile_space_down`` -- the MI355X dimension, the compiled tile variants the
+  library accepts for a problem, searched one GEMM at a time (the two launches' times add).
+
+``search`` sweeps a candidate list with a checkpoint after every record; ``refine_candidates`` and
+``pick_fastest`` serve tune mode's side-by-side re-timing of near-equal finalists.
 """
 from __future__ import annotations
 
-import itertools
 import math
+from dataclasses import dataclass, field
+
+RANKING_METRIC = "unprofiled_device_event_median_us"
+
+
+def rank_value(record):
+    """The record's ranking time, or None when it may not rank (not passed, or a median that is
+    missing, non-finite or not positive)."""
+    value = record.get("device_median_us")
+    if record.get("status") != "passed" or isinstance(value, bool) or not isinstance(value, (int, float)):
+        return None
+    return float(value) if math.isfinite(value) and value > 0 else None
+
+
+@dataclass
+class Leaderboard:
+    """Running best of one sweep over `scope` (a candidate list)."""
+
+    scope: list
+    configuration: dict | None = None
+    device_median_us: float | None = None
+    complete: bool = False
+    records: list = field(default_factory=list)
+
+    def add(self, record):
+        """Append an evaluated record; it takes the lead if it ranks and beats the current best."""
+        self.records.append(record)
+        value = rank_value(record)
+        if value is not None and (self.device_median_us is None or value < self.device_median_us):
+            self.configuration, self.device_median_us = record["configuration"], value
+
+    def state(self):
+        """The best_configs.json entry of this sweep (a fresh dict)."""
+        return {"configuration": self.configuration, "device_median_us": self.device_median_us,
+                "complete": self.complete, "ranking_metric": RANKING_METRIC, "scope": self.scope}
+
+
+def _distinct(values):
+    out = []
+    for value in values:
+        if value not in out:
+            out.append(value)
+    return out
 
 
 def combinations(up, down):
-    """[{'up_impl': u, 'down_impl': d}] over the de-duplicated product (performance/tune.py:6-9)."""
-    if not up or not down:
+    """The up x down implementation product as candidate dicts, duplicates dropped, order kept
+    (performance/tune.py:6-9); ValueError when either side is empty."""
+    ups, downs = _distinct(up), _distinct(down)
+    if not ups or not downs:
         raise ValueError("Search spaces must be non-empty")
-    return [{"up_impl": u, "down_impl": d}
-            for u, d in itertools.product(dict.fromkeys(up), dict.fromkeys(down))]
+    return [{"up_impl": u, "down_impl": d} for u in ups for d in downs]
+
+
+def search(configurations, evaluate, checkpoint=None, progress=print):
+    """Evaluate `configurations` in order; returns (records, best) (performance/tune.py:12-31).
+
+    Each record is evaluate(configuration) with the configuration attached.  checkpoint(records,
+    best) runs after every record -- so an interruption leaves what was measured, with best
+    marked incomplete -- and once more when the sweep is complete.
+    """
+    board = Leaderboard(list(configurations))
+    total = len(board.scope)
+    for position, configuration in enumerate(board.scope, start=1):
+        if progress is not None:
+            progress(f"[search {position}/{total}] {configuration}")
+        board.add(dict(evaluate(configuration), configuration=configuration))
+        if checkpoint is not None:
+            checkpoint(list(board.records), board.state())
+    board.complete = True
+    if checkpoint is not None:
+        checkpoint(list(board.records), board.state())
+    return list(board.records), board.state()
 
 
 def _applicable(problem, down, block_num, gelu, up_variant, down_variant):
@@ -57,7 +128,7 @@ def tile_space_down(problem, downs, up_variant, block_num, gelu="erf"):
     from .. import _lib
     nvar = _lib.load().ffn_mi355x_num_variants()
     return [{"up_impl": "basic", "down_impl": d, "up_variant": up_variant, "down_variant": dv}
-            for d in dict.fromkeys(downs) for dv in range(nvar)
+            for d in _distinct(downs) for dv in range(nvar)
             if _applicable(problem, d, block_num, gelu, up_variant, dv) is not None]
 
 
@@ -86,31 +157,3 @@ def pick_fastest(rows):
     if refined:
         return min(refined, key=lambda r: r["refined_median_us"])
     return min(passed, key=lambda r: r["device_median_us"])
-
-
-def search(configurations, evaluate, checkpoint=None):
-    """Evaluate every configuration; returns (records, best) (performance/tune.py:12-31).
-
-    best['configuration'] stays None unless some candidate passed with a finite,
-    positive device_median_us; checkpoint(records, best) runs after every candidate
-    and once more with best['complete'] set.
-    """
-    records = []
-    best = {"configuration": None, "device_median_us": None, "complete": False,
-            "ranking_metric": "unprofiled_device_event_median_us", "scope": configurations}
-    for index, configuration in enumerate(configurations, start=1):
-        print(f"[search] evaluating configuration {index}/{len(configurations)}: {configuration}",
-              flush=True)
-        row = dict(evaluate(configuration), configuration=configuration)
-        records.append(row)
-        value = row.get("device_median_us")
-        if (row["status"] == "passed" and isinstance(value, (int, float))
-                and math.isfinite(value) and value > 0
-                and (best["device_median_us"] is None or value < best["device_median_us"])):
-            best.update(configuration=configuration, device_median_us=value)
-        if checkpoint:
-            checkpoint(records, best)
-    best["complete"] = True
-    if checkpoint:
-        checkpoint(records, best)
-    return records, best

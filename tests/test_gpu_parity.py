@@ -348,6 +348,8 @@ def test_harness_manual_run_on_device(tmp_path):
         row = rows[0]
         assert row["device_median_us"] > 0 and len(row["device_samples_us"]) == 3
         assert row["accuracy"]["mean_rel"] < 0.01
+        # the staged rational-GELU golden (performance/run.py:130-131, :204 of the reference)
+        assert row["staged_accuracy"]["passed"] and row["staged_accuracy"]["mean_rel"] < 0.01
         assert row["task_duration_us"] is None or row["task_duration_us"] > 0
         assert row.get("profiler_path") or row.get("profiler_note")
         assert json.loads((run / "manifest.json").read_text())["device_executed"]

@@ -336,7 +336,10 @@ def test_tuning_table_rejects_bad_entries(tmp_path):
 
 
 @pytest.mark.parametrize("gelu", ["erf", "rational"])
-def test_harness_golden_matches_oracle(gelu):
+@pytest.mark.parametrize("staged", [False, True])
+def test_harness_golden_matches_oracle(gelu, staged):
+    """The harness's golden (plain and staged, erf and rational GELU) is the oracle's, bit for
+    bit: the same torch CPU FP32 operations in the same order."""
     import torch
     from ffn_optim_amd.performance.accuracy import compare, golden
     from oracle.reference import compare as oracle_compare, ffn_torch
@@ -344,10 +347,12 @@ def test_harness_golden_matches_oracle(gelu):
     x = torch.randn(3, 7, 40, generator=g).half()
     w1 = (torch.randn(72, 40, generator=g) * 40 ** -0.5).half()
     w2 = (torch.randn(24, 72, generator=g) * 72 ** -0.5).half()
-    ours = golden(x, w1, w2, gelu=gelu)
-    ref = ffn_torch(x, w1, w2, rational=(gelu == "rational"))
+    ours = golden(x, w1, w2, gelu=gelu, staged=staged)
+    ref = ffn_torch(x, w1, w2, rational=(gelu == "rational"), staged=staged)
     assert ours.shape == ref.shape and ours.dtype == ref.dtype
-    assert compare(ours, ref)["mean_rel"] < 1e-3
+    assert torch.equal(ours, ref)
+    if staged:
+        assert not torch.equal(ours, golden(x, w1, w2, gelu=gelu))
     noisy = (ref.float() * 1.2).to(ref.dtype)
     for a, b in ((ours, ref), (noisy, ref), (ref.float(), ref), (ref * float("nan"), ref)):
         ra, rb = compare(a, b), oracle_compare(a, b)
