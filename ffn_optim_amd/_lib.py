@@ -19,6 +19,8 @@ GELU_CODES = {"erf": 0, "rational": 1}
 ACTIVATION_CODES = {"gelu:erf": 0, "gelu:rational": 1, "silu": 2, "swiglu": 3}
 
 OK, EINVAL, ENOT_APPLICABLE, EUNAVAILABLE, EHIP, EDEVICE = 0, -1, -2, -3, -4, -5
+# FFN_MI355X_MAX_PITCH: the largest operand row pitch (elements) ffn_mi355x_set_operands accepts
+MAX_PITCH = 4_000_000
 
 
 class PlanStruct(ctypes.Structure):
@@ -42,20 +44,15 @@ class PlanStruct(ctypes.Structure):
 _P = ctypes.POINTER
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
-SIGNATURES = {
+# Entry points that load, query and plan: a library lacking one of them cannot serve this host
+# at all (load() raises LibraryMismatch, which prepare_ffn reports as DependencyUnavailable).
+CORE_SIGNATURES = {
     "ffn_mi355x_query": (_i, [_i, _P(_i), ctypes.c_char_p, _i]),
     "ffn_mi355x_make_plan": (_i, [_i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _P(PlanStruct)]),
     "ffn_mi355x_workspace_bytes": (_i, [_P(PlanStruct), _P(ctypes.c_size_t)]),
     "ffn_mi355x_workspace_counter_bytes": (_i, [_P(PlanStruct), _P(ctypes.c_size_t)]),
     "ffn_mi355x_set_operands": (_i, [_P(PlanStruct), _i, _i, _i, _i, _i, _i]),
     "ffn_mi355x_set_x_rows": (_i, [_P(PlanStruct), _i, _i, _i, _i, _i]),
-    "ffn_mi355x_run": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
-    "ffn_mi355x_run_noalloc": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp]),
-    "ffn_mi355x_run_ex": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
-    "ffn_mi355x_up_ex": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp]),
-    "ffn_mi355x_down_ex": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp]),
-    "ffn_mi355x_up": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp]),
-    "ffn_mi355x_down": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp]),
     "ffn_mi355x_num_variants": (_i, []),
     "ffn_mi355x_variant_info": (_i, [_i, _P(_i), _P(_i), _P(_i), _P(_i), _P(_i), _P(_i)]),
     "ffn_mi355x_variant_refill_waves": (_i, [_i]),
@@ -63,13 +60,52 @@ SIGNATURES = {
     "ffn_mi355x_strerror": (ctypes.c_char_p, [_i]),
     "ffn_mi355x_version": (ctypes.c_char_p, []),
 }
+# Launch entry points, bound when present: compile_kernel requires those a plan launches
+# through (require_entry_points), and a library without them fails there, the counterpart of
+# the reference's compile step failing (KernelCompilationError, ops/api.py:82-88).
+LAUNCH_SIGNATURES = {
+    "ffn_mi355x_run": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ffn_mi355x_run_noalloc": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ffn_mi355x_run_ex": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ffn_mi355x_up_ex": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ffn_mi355x_down_ex": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ffn_mi355x_up": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp]),
+    "ffn_mi355x_down": (_i, [_P(PlanStruct), _vp, _vp, _vp, _vp, _vp]),
+}
+SIGNATURES = {**CORE_SIGNATURES, **LAUNCH_SIGNATURES}
+
+
+class LibraryMismatch(OSError):
+    """The shared object loads but lacks entry points this host calls (a stale or foreign
+    build)."""
+
+
+def _bind(lib) -> list[str]:
+    """Set restype/argtypes of every entry point the library exports; returns the names of
+    the missing launch entry points.  A missing core entry point raises LibraryMismatch."""
+    missing_core, missing_launch = [], []
+    for table, missing in ((CORE_SIGNATURES, missing_core), (LAUNCH_SIGNATURES, missing_launch)):
+        for name, (res, args) in table.items():
+            try:
+                fn = getattr(lib, name)
+            except AttributeError:
+                missing.append(name)
+                continue
+            fn.restype, fn.argtypes = res, args
+    if missing_core:
+        raise LibraryMismatch(f"{lib._name} does not export {', '.join(missing_core)}; "
+                              "rebuild it with `python -m ffn_optim_amd.build`")
+    lib._ffn_missing_launch = tuple(missing_launch)
+    return missing_launch
+
 
 _lock = threading.Lock()
 _lib = None
 
 
 def load(path: Path | str | None = None):
-    """Load (once) and return the library; raises OSError if it cannot be loaded.
+    """Load (once) and return the library; raises OSError if it cannot be loaded, and
+    LibraryMismatch (an OSError) if it lacks a core entry point.
 
     torch is imported first: it loads its own copy of the HIP runtime by path, and the
     library's libamdhip64.so.7 dependency must then resolve (by soname) to that same copy.
@@ -81,13 +117,19 @@ def load(path: Path | str | None = None):
     with _lock:
         if _lib is None or path is not None:
             lib = ctypes.CDLL(str(path or LIBRARY_PATH), mode=ctypes.RTLD_LOCAL)
-            for name, (res, args) in SIGNATURES.items():
-                fn = getattr(lib, name)
-                fn.restype, fn.argtypes = res, args
+            _bind(lib)
             if path is not None:
                 return lib
             _lib = lib
         return _lib
+
+
+def require_entry_points(lib, names) -> None:
+    """RuntimeError naming the launch entry points of `names` that `lib` does not export."""
+    absent = [n for n in names if n in getattr(lib, "_ffn_missing_launch", ())]
+    if absent:
+        raise RuntimeError(f"{lib._name} does not export the launch entry point(s) "
+                           f"{', '.join(absent)}")
 
 
 def last_error() -> str:

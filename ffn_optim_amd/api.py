@@ -22,10 +22,12 @@ from .host.tiling import make_plan
 
 
 class KernelCompilationError(RuntimeError):
-    """Loading or binding the prebuilt kernels failed (ops/api.py:9-14).
+    """Binding the prebuilt kernels to a plan failed (ops/api.py:9-14): the library lacks a
+    launch entry point or a tile variant the plan needs.
 
-    Raised before any FFN launch; input preparation may already have run.
-    The original exception is chained.
+    Raised before any FFN launch and before the input copies.  The original exception is
+    chained.  (A library that is missing, unloadable or lacks a planning entry point is
+    reported earlier, as DependencyUnavailable.)
     """
 
 
@@ -112,6 +114,14 @@ def prepare_ffn(x, weight1, weight2, *, up_impl="basic", down_impl="basic", bloc
                      down_variant=down_variant)
     if block_num > cu_count:
         raise ValueError(f"block_num must not exceed the device CU count ({cu_count})")
+    # Binding needs the plan only, so it runs before any device work: a library that cannot
+    # launch this plan fails here, ahead of the input copies.
+    before = perf_counter()
+    try:
+        artifact, provenance = compile_kernel(plan)
+    except Exception as exc:
+        raise KernelCompilationError(f"{type(exc).__name__}: {exc}") from exc
+    compile_ms = (perf_counter() - before) * 1000
     with torch.cuda.device(x.device):
         stream = torch.cuda.current_stream()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -125,13 +135,8 @@ def prepare_ffn(x, weight1, weight2, *, up_impl="basic", down_impl="basic", bloc
         end.synchronize()
         auxiliary_ms = start.elapsed_time(end)
         tensors = tuple(t.data_ptr() for t in storage)
-        before = perf_counter()
-        try:
-            artifact, provenance = compile_kernel(plan)
-        except Exception as exc:
-            raise KernelCompilationError(f"{type(exc).__name__}: {exc}") from exc
         preparation = {"auxiliary_device_interval_ms": auxiliary_ms,
-                       "compile_wall_ms": (perf_counter() - before) * 1000}
+                       "compile_wall_ms": compile_ms}
     return PreparedFFN(plan, storage, tensors, artifact, provenance, preparation, stream)
 
 

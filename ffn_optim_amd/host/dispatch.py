@@ -76,7 +76,9 @@ def compile_kernel(plan):
 
     The counterpart of the reference's compile step: the kernels are already
     compiled for gfx950, so this loads the library and binds the plan.  The
-    artifact launches up + down on the stream it is given.
+    artifact launches up + down on the stream it is given.  Raises RuntimeError when
+    the library lacks a launch entry point or the plan's tile variants (prepare_ffn
+    reports it as KernelCompilationError).
     """
     Selection(plan.selection.up_impl, plan.selection.down_impl).require_available()
     provenance = verify_dependency()
@@ -84,6 +86,11 @@ def compile_kernel(plan):
 
     lib = _lib.load()
     native = plan.native
+    # binding: the entry points this artifact launches through, and the plan's tile variants
+    _lib.require_entry_points(lib, ("ffn_mi355x_run", "ffn_mi355x_run_ex"))
+    for variant in (native.up_variant, native.down_variant):
+        if not 0 <= variant < lib.ffn_mi355x_num_variants():
+            raise RuntimeError(f"tile variant {variant} is not compiled into {_lib.LIBRARY_PATH.name}")
     plan_ref = ctypes.byref(native)
     run, run_ex = lib.ffn_mi355x_run, lib.ffn_mi355x_run_ex
 

@@ -391,6 +391,22 @@ def test_row_grid_addresses_every_row():
         assert row_grid(v, v.shape[-1]) is None, name
 
 
+def test_row_grid_copies_rows_past_the_largest_pitch():
+    """A column slice of rows wider than the library's largest pitch is copied (None), not
+    handed to set_operands, which would refuse it; at the largest pitch it is read in place.
+    The Python bound is the header's FFN_MI355X_MAX_PITCH, and the library enforces it."""
+    from ffn_optim_amd.host.inputs import row_grid
+    header = (Path(__file__).resolve().parent.parent / "include" / "ffn_mi355x.h").read_text()
+    assert int(re.search(r"#define FFN_MI355X_MAX_PITCH (\d+)", header).group(1)) == _lib.MAX_PITCH
+    for width, want in ((_lib.MAX_PITCH, ("pitch", _lib.MAX_PITCH)), (_lib.MAX_PITCH + 16, None)):
+        base = torch.empty((2, width), dtype=torch.bfloat16)
+        assert row_grid(base[:, :1024], 1024) == want
+    plan = _lib.make_plan(64, 1024, 1024, 1024, _lib.BF16, "basic", "erf", 256, m=2)
+    _lib.set_operands(plan, 1024, 1024, 1024, _lib.MAX_PITCH, 1024, 1024)
+    with pytest.raises(ValueError):
+        _lib.set_operands(plan, 1024, 1024, 1024, _lib.MAX_PITCH + 8, 1024, 1024)
+
+
 def test_set_x_rows_validates_grid():
     """ffn_mi355x_set_x_rows accepts a grid that tiles m with 16-byte strides, keeps it through
     set_operands, and rejects the rest without touching the plan."""
@@ -539,6 +555,43 @@ def test_prepare_ffn_reports_an_unloadable_library(tmp_path, monkeypatch, damage
     x, a, b = torch.zeros(2, 16).half(), torch.zeros(64, 16).half(), torch.zeros(8, 64).half()
     with pytest.raises(DependencyUnavailable, match="libffn_mi355x.so"):
         api.prepare_ffn(x, a, b)
+
+
+@pytest.mark.parametrize("plans", [False, True])
+def test_prepare_ffn_reports_a_partial_library(tmp_path, monkeypatch, plans):
+    """A library that loads but lacks entry points (a stale or partial build, here a gcc-built
+    stand-in): without its planning entry points prepare_ffn reports DependencyUnavailable
+    naming the missing symbol (ops/host/dispatch.py:69-83); with them but no launch entry
+    point, binding the plan fails and prepare_ffn raises KernelCompilationError with the cause
+    chained (ops/api.py:9-14, 82-88), before any input copy."""
+    import subprocess
+    import torch
+    from ffn_optim_amd import _lib, api
+    from ffn_optim_amd.host import inputs
+    from ffn_optim_amd.host.dispatch import DependencyUnavailable
+    lib_path = tmp_path / "libffn_mi355x.so"
+    here = Path(__file__).resolve().parent
+    cmd = ["gcc", "-shared", "-fPIC", "-Wall", "-Werror", "-I", str(here.parent / "include"),
+           "-o", str(lib_path), str(here / "stubs" / "partial_abi.c")]
+    if not plans:
+        cmd.insert(1, "-DPARTIAL_ABI_NO_PLAN")
+    subprocess.run(cmd, check=True)
+    monkeypatch.setattr(_lib, "LIBRARY_PATH", lib_path)
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(api, "validate_tensors",
+                        lambda *a, **k: inputs.validate_tensors(*a, **dict(k, require_device=False)))
+    monkeypatch.setattr(torch.cuda, "current_device", lambda: 0)
+    copies = []
+    monkeypatch.setattr(api, "prepare_storage", lambda *a, **k: copies.append(1))
+    x, a, b = torch.zeros(2, 16).half(), torch.zeros(64, 16).half(), torch.zeros(8, 64).half()
+    if not plans:
+        with pytest.raises(DependencyUnavailable, match="ffn_mi355x_make_plan"):
+            api.prepare_ffn(x, a, b)
+    else:
+        with pytest.raises(api.KernelCompilationError, match="ffn_mi355x_run") as info:
+            api.prepare_ffn(x, a, b, down_impl="basic")
+        assert isinstance(info.value.__cause__, RuntimeError)
+    assert copies == []
 
 
 def test_tile_keeps_the_reference_l1_names():
