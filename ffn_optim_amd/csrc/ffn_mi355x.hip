@@ -279,7 +279,8 @@ int down_depth(const ffn_mi355x_plan* p) { return p->h % 8 == 0 ? p->h : p->hp; 
 // Largest operand row pitch (elements).  The kernels address a macro tile's rows with 32-bit
 // buffer offsets: up to 256 rows of a pitch plus the K offset, (256 + 1) * pitch * 2 bytes,
 // must stay below 2^31, the offset that marks a zero-filled chunk.
-constexpr int kMaxPitch = 4000000;
+constexpr int kMaxPitch = FFN_MI355X_MAX_PITCH;
+static_assert((256LL + 1) * kMaxPitch * 2 < (1LL << 31), "a tile's row offsets stay below 2^31");
 
 bool pitch_ok(int ld) { return ld % 8 == 0 && ld <= kMaxPitch; }
 

@@ -130,9 +130,11 @@ def row_grid(x, k):
     s2)) when two or three are left (a permuted view such as a [B, S, K] tensor read as
     [S, B, K]: row (i0, i1, i2) of a [m / (d1*d2), d1, d2] grid starts at i0*s0 + i1*s1 + i2*s2),
     or None when the view must be copied: K not contiguous or not a multiple of 8, a stride or
-    the base off a 16-byte boundary, more than three dims left, or rows spread over 2^31 bytes
-    or more.  No counterpart in the reference, which copies every X (ops/host/inputs.py:74-90).
+    the base off a 16-byte boundary, more than three dims left, rows spread over 2^31 bytes
+    or more, or a single pitch above the library's largest (_lib.MAX_PITCH).  No counterpart
+    in the reference, which copies every X (ops/host/inputs.py:74-90).
     """
+    from .._lib import MAX_PITCH
     if k % 8 != 0 or x.stride(-1) != 1 or (x.data_ptr() % 16) != 0:
         return None
     dims = [(n, st) for n, st in zip(x.shape[:-1], x.stride()[:-1]) if n != 1]
@@ -151,7 +153,7 @@ def row_grid(x, k):
     if span > MAX_GATHER_SPAN:
         return None
     if len(merged) == 1 and merged[0][1] >= k:
-        return ("pitch", merged[0][1])
+        return ("pitch", merged[0][1]) if merged[0][1] <= MAX_PITCH else None
     merged = [(1, 0)] * (3 - len(merged)) + merged
     (_, s0), (d1, s1), (d2, s2) = merged
     return ("grid", (d1, d2, s0, s1, s2))

@@ -44,6 +44,11 @@ extern "C" {
                                       in 32-row blocks (rows 64b..64b+31 = gate rows 32b..32b+31,
                                       rows 64b+32..64b+63 = up rows 32b..32b+31), zero past h */
 
+/* Largest operand row pitch, in elements, that ffn_mi355x_set_operands accepts: a macro tile's
+ * rows are addressed with 32-bit buffer offsets, and (256 + 1) rows of this pitch in 2-byte
+ * elements stay below 2^31, the offset that marks a zero-filled chunk. */
+#define FFN_MI355X_MAX_PITCH 4000000
+
 /* return codes */
 #define FFN_MI355X_OK 0
 #define FFN_MI355X_EINVAL (-1)          /* ValueError */
@@ -118,7 +123,8 @@ int ffn_mi355x_make_plan(int m, int mp, int kp, int hp, int np, int dtype, int d
  * through the kernels' range checks, and hidden columns [h, hp) are written as GELU(0) = 0.
  * k must be a multiple of 8 or equal kp; with h not a multiple of 8, W2 must span hp
  * columns (ldw2 >= hp, zero past h).  No counterpart in the reference, whose prepare step
- * always copies into padded buffers (ops/host/inputs.py:74-90).  EINVAL on a bad layout. */
+ * always copies into padded buffers (ops/host/inputs.py:74-90).  EINVAL on a bad layout,
+ * including a pitch above FFN_MI355X_MAX_PITCH. */
 int ffn_mi355x_set_operands(ffn_mi355x_plan* plan, int k, int h, int n, int ldx, int ldw1, int ldw2);
 
 /* Reads X in place as a strided view instead of rows at one pitch: the plan's m rows form a
