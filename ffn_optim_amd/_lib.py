@@ -34,7 +34,8 @@ class PlanStruct(ctypes.Structure):
         "down_sk_tiles", "down_slots_per_wg")] + [("workspace_bytes", ctypes.c_size_t)] + [
         (name, ctypes.c_int) for name in ("k", "h", "n", "ldx", "ldw1", "ldw2",
                                           "up_k_iters", "up_sk_tiles", "up_slots_per_wg",
-                                          "x_d1", "x_d2", "x_s0", "x_s1", "x_s2")] + [
+                                          "x_d1", "x_d2", "x_s0", "x_s1", "x_s2",
+                                          "single_launch")] + [
         ("stamp", ctypes.c_ulonglong)]
 
     def to_dict(self):
@@ -53,6 +54,7 @@ CORE_SIGNATURES = {
     "ffn_mi355x_workspace_counter_bytes": (_i, [_P(PlanStruct), _P(ctypes.c_size_t)]),
     "ffn_mi355x_set_operands": (_i, [_P(PlanStruct), _i, _i, _i, _i, _i, _i]),
     "ffn_mi355x_set_x_rows": (_i, [_P(PlanStruct), _i, _i, _i, _i, _i]),
+    "ffn_mi355x_set_single_launch": (_i, [_P(PlanStruct), _i]),
     "ffn_mi355x_num_variants": (_i, []),
     "ffn_mi355x_variant_info": (_i, [_i, _P(_i), _P(_i), _P(_i), _P(_i), _P(_i), _P(_i)]),
     "ffn_mi355x_variant_refill_waves": (_i, [_i]),
@@ -191,6 +193,11 @@ def workspace_counter_bytes(plan: PlanStruct) -> int:
     n = ctypes.c_size_t()
     check(load().ffn_mi355x_workspace_counter_bytes(ctypes.byref(plan), ctypes.byref(n)))
     return n.value
+
+
+def set_single_launch(plan: PlanStruct, on: bool) -> None:
+    """Run the plan's FFN as one launch or as two (ffn_mi355x_set_single_launch)."""
+    check(load().ffn_mi355x_set_single_launch(ctypes.byref(plan), 1 if on else 0))
 
 
 def set_x_rows(plan: PlanStruct, d1, d2, s0, s1, s2) -> None:

@@ -83,7 +83,7 @@ def _current_stream_handle(device):
 
 def prepare_ffn(x, weight1, weight2, *, up_impl="basic", down_impl="basic", block_num=None,
                 layout="linear", gelu="erf", up_variant=None, down_variant=None, activation="gelu",
-                bias1=None, bias2=None, _alias=False):
+                bias1=None, bias2=None, single_launch=None, _alias=False):
     """Validate, plan, check the device, pad/contiguise and bind the kernels; no FFN launch.
 
     Follows ops/api.py:48-89.  Padding and contiguisation are auxiliary device
@@ -96,6 +96,10 @@ def prepare_ffn(x, weight1, weight2, *, up_impl="basic", down_impl="basic", bloc
     biases bias1 ([H] or [2H]) and bias2 ([N]), given together, select the other EagleFFN
     paths, Y = act(X W1^T + b1) W2^T + b2 (spec/MindIE-SD EagleFFN算子实现分析.md:17-71); the
     defaults are the reference's operator.  storage then ends with the two bias buffers.
+
+    single_launch: True runs the FFN as one launch (NotApplicable where no single-launch kernel
+    is compiled for the plan's tile pair); None and False keep the two launches, which measured
+    faster on every workload the single launch serves.
     """
     from .host.dispatch import compile_kernel
     from . import _lib
@@ -114,6 +118,8 @@ def prepare_ffn(x, weight1, weight2, *, up_impl="basic", down_impl="basic", bloc
                      down_variant=down_variant)
     if block_num > cu_count:
         raise ValueError(f"block_num must not exceed the device CU count ({cu_count})")
+    if single_launch is not None:
+        _lib.set_single_launch(plan.native, bool(single_launch))
     # Binding needs the plan only, so it runs before any device work: a library that cannot
     # launch this plan fails here, ahead of the input copies.
     before = perf_counter()

@@ -1,8 +1,9 @@
 """Build recipe of ``libffn_mi355x.so`` for gfx950 (MI355X).
 
 The library is compiled ahead of time, in-tree, with ``hipcc``: one object per
-(storage type, tile variant) pair from ``csrc/ffn_kernels.hip`` plus the host
-object ``csrc/ffn_mi355x.hip``, linked into ``ffn_optim_amd/libffn_mi355x.so``.
+(storage type, tile variant) pair from ``csrc/ffn_kernels.hip``, one per (storage
+type, single-launch tile pair) from ``csrc/ffn_fused.hip``, plus the host object
+``csrc/ffn_mi355x.hip``, linked into ``ffn_optim_amd/libffn_mi355x.so``.
 It replaces the reference's just-in-time ``tla.compile`` of ``ops/kernel/ffn.py``
 (ops/host/dispatch.py:97-116).
 
@@ -50,6 +51,13 @@ def variant_ids() -> list[int]:
     return ids
 
 
+def fused_pairs() -> list[tuple[int, int]]:
+    """(up, down) variant pairs compiled as a single-launch FFN (FFN_FUSED_PAIRS)."""
+    text = (CSRC / "ffn_variants.hpp").read_text()
+    m = re.search(r"^#define FFN_FUSED_PAIRS\(X\)(.*)$", text, re.M)
+    return [(int(a), int(b)) for a, b in re.findall(r"X\((\d+),\s*(\d+)\)", m.group(1))] if m else []
+
+
 def source_revision() -> str:
     digest = hashlib.sha256()
     for path in sorted(CSRC.glob("*")) + sorted(INCLUDE.glob("*.h")):
@@ -79,6 +87,10 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
             obj = BUILD_DIR / f"ffn_kernels_d{dt}_v{vid}.o"
             units.append([cc, *DEVICE_FLAGS, *inc, f"-DFFN_DT={dt}", f"-DFFN_VARIANT={vid}",
                           "-c", str(CSRC / "ffn_kernels.hip"), "-o", str(obj)])
+        for up, down in fused_pairs():
+            obj = BUILD_DIR / f"ffn_fused_d{dt}_u{up}_n{down}.o"
+            units.append([cc, *DEVICE_FLAGS, *inc, f"-DFFN_DT={dt}", f"-DFFN_UPV={up}", f"-DFFN_DNV={down}",
+                          "-c", str(CSRC / "ffn_fused.hip"), "-o", str(obj)])
     host_obj = BUILD_DIR / "ffn_mi355x.o"
     units.append([cc, *DEVICE_FLAGS, *inc, f'-DFFN_MI355X_REVISION="{rev}"',
                   "-c", str(CSRC / "ffn_mi355x.hip"), "-o", str(host_obj)])

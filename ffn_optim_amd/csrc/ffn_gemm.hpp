@@ -74,7 +74,26 @@ struct GemmParams {
     // the rows lie within a_bytes of a.  a_gather = 0: row r starts at r*lda.
     int a_gather, a_d1, a_d2, a_s0, a_s1, a_s2;
     unsigned a_bytes;
+    // Arrival counters of the FFN's other GEMM (the Stream-K down's, in an up launch; a split up
+    // GEMM's, in a down launch), written as zeros ahead of any tile: a counter region left dirty
+    // (never cleared, or by an interrupted or overlapping call) is repaired by the launch before
+    // the one that counts on it.
+    unsigned* clear_words;
+    int clear_count;
 };
+
+// Counter words of a single-launch FFN (ffn_fused.hip), in the workspace's counter region; zero
+// between launches (the last workgroup to leave clears them) but for the error word:
+//   [0, 8)             ticket queue of each XCD
+//   [8]                workgroups that have left
+//   [9]                error word: set when a down tile gave up waiting for its row block
+//   [16, 16 + R)       up tiles stored, per up row block
+struct FusedParams {
+    unsigned* ctr;
+    int ratio;       // down row blocks per up row block (BM_up / BM_down)
+    int spin_limit;  // polls of a row-block counter before a down tile gives up
+};
+constexpr int kFusedLeft = 8, kFusedError = 9, kFusedReady = 16;
 
 // SYNCQ_: MFMA slot of a stage's last k-step after which the stage wait + barrier is placed
 // (-1: end of the first block of B).  DMAKS_: with two stages, the k-steps at the start of an
@@ -406,7 +425,11 @@ struct UnitWalker {
 
 // ISSUE: this wave issues its share of the refill DMA (false for the waves at or past C::DW).
 // MMA: this wave holds a wave tile (false for the refill waves of a tile with C::PROD > 0).
-template <int DT, class C, bool GA = false, bool ISSUE = true, bool MMA = true>
+// Both are the calling wave's roles and have no default: an engine is built only inside
+// with_wave_roles (below), which gives every wave the roles of its number.  (The refill blocks
+// of wave w are w * A_PW + D: a wave at or past C::DW given ISSUE would address rows past the
+// tile, which on the SALU-addressed refill are reads past the operand.)
+template <int DT, class C, bool GA, bool ISSUE, bool MMA>
 struct Engine {
     static constexpr int FM = C::FM, FN = C::FN, NT = C::NT, S = C::STAGES, KS = C::KSTEPS;
     static_assert(KS % 2 == 0, "fragment double-buffer assumes an even number of k-steps per wave");
@@ -1248,9 +1271,28 @@ struct Engine {
 template <class C, int EPI, bool SK>
 constexpr bool epi_in_regs() { return EPI != EPI_STORE || SK || !C::OUT_POW2 || C::PROD > 0; }
 
+// The wave roles of a tile: with refill-only waves (C::PROD > 0) waves [0, PROD) issue the whole
+// refill and hold no wave tile, and the others hold wave tiles and issue no DMA; otherwise every
+// wave holds a wave tile and waves [0, C::DW) issue the refill.  Calls
+// body.template run<ISSUE, MMA>() with the calling wave's roles, a wave-uniform choice made once.
+// Every kernel builds its engines inside a body run here.
+template <class C, class Body>
+__device__ __forceinline__ void with_wave_roles(Body& body) {
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    if constexpr (C::PROD > 0) {
+        if (wave < C::PROD) body.template run<true, false>();
+        else body.template run<false, true>();
+    } else if constexpr (C::DW == C::NW) {
+        body.template run<true, true>();
+    } else {
+        if (wave < C::DW) body.template run<true, true>();
+        else body.template run<false, true>();
+    }
+}
+
 // One wave's walk over its workgroup's units, in the refill role ISSUE and tile role MMA.
 // Every wave of the workgroup passes the same barriers whatever its roles.
-template <int DT, class C, int EPI, bool SK, bool FASTK, bool GATHER, bool ISSUE, bool MMA = true>
+template <int DT, class C, int EPI, bool SK, bool FASTK, bool GATHER, bool ISSUE, bool MMA>
 __device__ __forceinline__ void walk_units(const GemmParams& p, lds_char* smem, int v, int G) {
     constexpr bool EPI_IN_REGS = epi_in_regs<C, EPI, SK>();
     // the refill waves skip the epilogue's data: a register epilogue or a split piece's partial
@@ -1284,6 +1326,15 @@ __device__ __forceinline__ void walk_units(const GemmParams& p, lds_char* smem, 
     }
 }
 
+template <int DT, class C, int EPI, bool SK, bool FASTK, bool GATHER>
+struct WalkBody {
+    const GemmParams& p;
+    lds_char* smem;
+    int v, G;
+    template <bool ISSUE, bool MMA>
+    __device__ __forceinline__ void run() { walk_units<DT, C, EPI, SK, FASTK, GATHER, ISSUE, MMA>(p, smem, v, G); }
+};
+
 // Persistent GEMM: every workgroup walks its units (whole tiles, then for Stream-K its split
 // iterations) with the DMA of the next unit overlapping the epilogue of the current one.
 // Split pieces that share a tile publish FP32 partials; the last to arrive finishes the tile.
@@ -1309,18 +1360,10 @@ __global__ void __launch_bounds__(C::NT) ffn_gemm_kernel(GemmParams p) {
             *(u32x4*)((char*)p.c + ((size_t)r * (size_t)p.ldc + (size_t)c * 8) * 2) = u32x4{0u, 0u, 0u, 0u};
         }
     }
-    lds_char* smem = (lds_char*)smem_raw;
-    if constexpr (C::PROD > 0) {
-        if (__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) < C::PROD)
-            walk_units<DT, C, EPI, SK, FASTK, GATHER, true, false>(p, smem, v, G);
-        else
-            walk_units<DT, C, EPI, SK, FASTK, GATHER, false, true>(p, smem, v, G);
-    } else if constexpr (C::DW == C::NW)
-        walk_units<DT, C, EPI, SK, FASTK, GATHER, true>(p, smem, v, G);
-    else if (__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) < C::DW)
-        walk_units<DT, C, EPI, SK, FASTK, GATHER, true>(p, smem, v, G);
-    else
-        walk_units<DT, C, EPI, SK, FASTK, GATHER, false>(p, smem, v, G);
+    for (int i = g * C::NT + (int)threadIdx.x; i < p.clear_count; i += G * C::NT)
+        __hip_atomic_store(p.clear_words + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    WalkBody<DT, C, EPI, SK, FASTK, GATHER> body{p, (lds_char*)smem_raw, v, G};
+    with_wave_roles<C>(body);
 }
 
 }  // namespace ffn

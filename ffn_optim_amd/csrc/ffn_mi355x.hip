@@ -36,6 +36,16 @@ typedef hipError_t (*ffn_launch_fn)(int role, const ffn::GemmParams* p, int grid
 FFN_VARIANTS(FFN_DECLARE_LAUNCHERS)
 #undef FFN_DECLARE_LAUNCHERS
 
+typedef hipError_t (*ffn_fused_fn)(int role, const ffn::GemmParams* pu, const ffn::GemmParams* pd,
+                                   const ffn::FusedParams* f, int grid, hipStream_t stream);
+#define FFN_DECLARE_FUSED(u, d)                                                                          \
+    extern "C" hipError_t ffn_fused_d0_u##u##_n##d(int, const ffn::GemmParams*, const ffn::GemmParams*, \
+                                                   const ffn::FusedParams*, int, hipStream_t);          \
+    extern "C" hipError_t ffn_fused_d1_u##u##_n##d(int, const ffn::GemmParams*, const ffn::GemmParams*, \
+                                                   const ffn::FusedParams*, int, hipStream_t);
+FFN_FUSED_PAIRS(FFN_DECLARE_FUSED)
+#undef FFN_DECLARE_FUSED
+
 namespace {
 
 struct Variant {
@@ -59,6 +69,20 @@ const Variant kVariants[] = {FFN_VARIANTS(FFN_VARIANT_ROW)};
 #undef FFN_VARIANT_ROW
 constexpr int kNumVariants = (int)(sizeof(kVariants) / sizeof(kVariants[0]));
 static_assert(kNumVariants == FFN_NUM_VARIANTS, "variant table");
+
+// Single-launch FFN kernels of the compiled (up, down) variant pairs (ffn_fused.hip).
+struct FusedPair {
+    int up, down;
+    ffn_fused_fn launch[2];  // [dtype]
+};
+#define FFN_FUSED_ROW(u, d) {u, d, {ffn_fused_d0_u##u##_n##d, ffn_fused_d1_u##u##_n##d}},
+const FusedPair kFusedPairs[] = {FFN_FUSED_PAIRS(FFN_FUSED_ROW)};
+#undef FFN_FUSED_ROW
+const FusedPair* fused_pair(int up, int down) {
+    for (const FusedPair& f : kFusedPairs)
+        if (f.up == up && f.down == down) return &f;
+    return nullptr;
+}
 
 thread_local std::string g_error;
 
@@ -350,7 +374,7 @@ unsigned long long plan_stamp(const ffn_mi355x_plan* p) {
                         p->down_bk, p->up_tiles, p->up_grid, p->down_tiles, p->down_grid, p->down_k_iters,
                         p->down_dp_tiles, p->down_sk_tiles, p->down_slots_per_wg, p->k, p->h, p->n, p->ldx,
                         p->ldw1, p->ldw2, p->up_k_iters, p->up_sk_tiles, p->up_slots_per_wg,
-                        p->x_d1, p->x_d2, p->x_s0, p->x_s1, p->x_s2};
+                        p->x_d1, p->x_d2, p->x_s0, p->x_s1, p->x_s2, p->single_launch};
     for (int v : ints) mix((unsigned long long)(unsigned)v);
     mix((unsigned long long)p->workspace_bytes);
     return h;
@@ -374,6 +398,35 @@ bool valid_plan(const ffn_mi355x_plan* p) {
 // plan, so one zero-filled workspace serves any plans in turn: no plan's slots overlap another
 // plan's counters.
 size_t flags_bytes(const ffn_mi355x_plan*) { return kCounterBytes; }
+
+// Arrival counters (one word per split tile and wave): the Stream-K down's from the start of the
+// counter region, a split up GEMM's from its end, so that each GEMM's launch can clear the
+// other's (GemmParams::clear_words) without touching its own.
+size_t down_counter_words(const ffn_mi355x_plan* p) {
+    return p->down_impl == FFN_MI355X_DOWN_STREAMK ? (size_t)p->down_sk_tiles * kVariants[p->down_variant].nw : 0;
+}
+size_t up_counter_words(const ffn_mi355x_plan* p) {
+    return p->up_sk_tiles > 0 ? (size_t)p->up_sk_tiles * kVariants[p->up_variant].nw : 0;
+}
+unsigned* up_counters(const ffn_mi355x_plan* p, void* ws) {
+    return (unsigned*)ws + (kCounterBytes / 4 - up_counter_words(p));
+}
+
+
+// A plan can run as one launch (ffn_fused.hip): a compiled kernel for its tile pair, a Basic down,
+// an unsplit up GEMM with the GELU epilogue (its K within the SALU-addressed refill), at least one
+// up row block per XCD and whole down row blocks per up row block, and room in the counter
+// region for the queues and the row-block counters.
+bool fused_ok(const ffn_mi355x_plan* p) {
+    if (!fused_pair(p->up_variant, p->down_variant)) return false;
+    const Variant& U = kVariants[p->up_variant];
+    const Variant& D = kVariants[p->down_variant];
+    const long long rbs = cdiv(p->m, U.bm);
+    return p->down_impl == FFN_MI355X_DOWN_BASIC && p->up_sk_tiles == 0 &&
+           (p->activation == FFN_MI355X_GELU_ERF || p->activation == FFN_MI355X_GELU_RATIONAL) &&
+           U.nw + U.prod == D.nw + D.prod && U.bm % D.bm == 0 && rbs >= 8 &&
+           ffn::kFusedReady + rbs <= (long long)(kCounterBytes / 4) && fast_dma_for(p->kp);
+}
 
 int launch(const Variant& v, int dtype, int role, const ffn::GemmParams& gp, int grid,
            void* stream) {
@@ -509,6 +562,16 @@ int ffn_mi355x_make_plan(int m, int mp, int kp, int hp, int np, int dtype, int d
     }
     if (up_ws > plan->workspace_bytes) plan->workspace_bytes = up_ws;
     if (plan->workspace_bytes > 0) plan->workspace_bytes += flags_bytes(plan);
+    // The single launch is opt-in (ffn_mi355x_set_single_launch): measured against the two launches
+    // of the same tile pair it was slower on every workload it serves (aligned mid-size 78.6
+    // against 72.0 us, unaligned 45.4 against 30.2, DiT-size 1065 against 979).  A plan that can
+    // take it reserves the counter region, so its workspace serves either form.
+    plan->single_launch = 0;
+    if (fused_ok(plan) && plan->workspace_bytes < flags_bytes(plan)) plan->workspace_bytes = flags_bytes(plan);
+    if (up_counter_words(plan) + down_counter_words(plan) > kCounterBytes / 4)
+        return fail(FFN_MI355X_ENOT_APPLICABLE, "the split tiles of the two GEMMs need more arrival counters "
+                    "(%zu) than the workspace holds (%zu)", up_counter_words(plan) + down_counter_words(plan),
+                    kCounterBytes / 4);
     // the kernels address partial slots with 32-bit buffer offsets
     if (plan->workspace_bytes >= (size_t)1 << 31)
         return fail(FFN_MI355X_EINVAL, "workspace of %zu bytes exceeds 2 GiB", plan->workspace_bytes);
@@ -553,6 +616,20 @@ int ffn_mi355x_set_x_rows(ffn_mi355x_plan* plan, int d1, int d2, int s0, int s1,
     return ok();
 }
 
+int ffn_mi355x_set_single_launch(ffn_mi355x_plan* plan, int on) {
+    if (!plan) return fail(FFN_MI355X_EINVAL, "plan must not be NULL");
+    if (!valid_plan(plan)) return fail(FFN_MI355X_EINVAL, "invalid plan");
+    if (on && !fused_ok(plan))
+        return fail(FFN_MI355X_ENOT_APPLICABLE, "no single-launch kernel for this plan (tile pair %d/%d, %s down)",
+                    plan->up_variant, plan->down_variant,
+                    plan->down_impl == FFN_MI355X_DOWN_BASIC ? "Basic" : "Stream-K");
+    ffn_mi355x_plan t = *plan;
+    t.single_launch = on ? 1 : 0;
+    t.stamp = plan_stamp(&t);
+    *plan = t;
+    return ok();
+}
+
 int ffn_mi355x_workspace_bytes(const ffn_mi355x_plan* plan, size_t* bytes) {
     if (!plan || !bytes) return fail(FFN_MI355X_EINVAL, "NULL argument");
     *bytes = plan->workspace_bytes;
@@ -570,9 +647,9 @@ int ffn_mi355x_workspace_counter_bytes(const ffn_mi355x_plan* plan, size_t* byte
 
 namespace {
 
-void set_workspace(ffn::GemmParams& gp, const ffn_mi355x_plan* plan, void* ws) {
+void set_workspace(ffn::GemmParams& gp, const ffn_mi355x_plan* plan, void* ws, bool up) {
     const size_t f = flags_bytes(plan);
-    gp.sk_flags = (unsigned*)ws;
+    gp.sk_flags = up ? up_counters(plan, ws) : (unsigned*)ws;
     gp.ws = (float*)((char*)ws + f);
     gp.ws_bytes = (unsigned)(plan->workspace_bytes - f);
 }
@@ -582,8 +659,9 @@ void set_workspace(ffn::GemmParams& gp, const ffn_mi355x_plan* plan, void* ws) {
 // Rows of W1 a plan reads: the logical H, or for SwiGLU the 2 hp interleaved gate and up rows.
 long long w1_rows(const ffn_mi355x_plan* p) { return p->activation == FFN_MI355X_SWIGLU ? 2LL * p->hp : p->h; }
 
+// built: fill *built and *role_out with the launch of an unsplit up GEMM instead of launching it.
 int run_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, const void* b1, void* hidden, void* ws,
-           bool ws_scratch, void* hip_stream) {
+           bool ws_scratch, void* hip_stream, ffn::GemmParams* built = nullptr, int* role_out = nullptr) {
     if (!valid_plan(plan)) return fail(FFN_MI355X_EINVAL, "invalid plan");
     if (!x || !w1 || !hidden) return fail(FFN_MI355X_EINVAL, "NULL device buffer");
     if (!aligned16(x) || !aligned16(w1) || !aligned16(hidden) || (ws && !aligned16(ws)) || (b1 && !aligned16(b1)))
@@ -600,7 +678,9 @@ int run_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, const voi
         (rc = check_span("w1", w1, span_bytes(rows, plan->ldw1, plan->k))) != FFN_MI355X_OK ||
         (b1 && (rc = check_span("bias1", b1, (size_t)rows * 2u)) != FFN_MI355X_OK) ||
         (rc = check_span("hidden", hidden, span_bytes(plan->mp, plan->hp, plan->hp))) != FFN_MI355X_OK ||
-        (split && !ws_scratch && (rc = check_span("ws", ws, plan->workspace_bytes)) != FFN_MI355X_OK))
+        (split && !ws_scratch && (rc = check_span("ws", ws, plan->workspace_bytes)) != FFN_MI355X_OK) ||
+        (!split && ws && !ws_scratch && down_counter_words(plan) > 0 &&
+         (rc = check_span("ws", ws, flags_bytes(plan))) != FFN_MI355X_OK))
         return rc;
     const Variant& U = kVariants[plan->up_variant];
     ffn::GemmParams gp;
@@ -625,6 +705,12 @@ int run_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, const voi
         gp.a_s0 = plan->x_s0, gp.a_s1 = plan->x_s1, gp.a_s2 = plan->x_s2;
         gp.a_bytes = (unsigned)x_span;
     }
+    if (ws && down_counter_words(plan) > 0) {
+        // the Stream-K down that follows counts on zero counters: clear them here
+        gp.clear_words = (unsigned*)ws;
+        gp.clear_count = (int)down_counter_words(plan);
+    }
+    if (split && built) return fail(FFN_MI355X_EINVAL, "a split up GEMM does not run in a single launch");
     if (split) {
         // every tile split (no whole tiles): FP32 partials; the last piece of a tile applies the
         // activation
@@ -634,7 +720,7 @@ int run_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, const voi
         gp.sk_q = (int)(total / plan->up_grid);
         gp.sk_r = (int)(total % plan->up_grid);
         gp.slots_per_wg = plan->up_slots_per_wg;
-        set_workspace(gp, plan, ws);
+        set_workspace(gp, plan, ws, true);
         const int role = plan->activation == FFN_MI355X_GELU_ERF        ? FFN_ROLE_UP_SPLIT_ERF
                          : plan->activation == FFN_MI355X_GELU_RATIONAL ? FFN_ROLE_UP_SPLIT_RATIONAL
                                                                         : FFN_ROLE_UP_SPLIT_SILU;
@@ -644,12 +730,17 @@ int run_up(const ffn_mi355x_plan* plan, const void* x, const void* w1, const voi
                      : plan->activation == FFN_MI355X_GELU_RATIONAL ? FFN_ROLE_UP_RATIONAL
                      : plan->activation == FFN_MI355X_SILU          ? FFN_ROLE_UP_SILU
                                                                     : FFN_ROLE_UP_SWIGLU;
+    if (built) {
+        *built = gp, *role_out = role;
+        return ok();
+    }
     return launch(U, plan->dtype, role, gp, plan->up_grid, hip_stream);
 }
 
 // Down GEMM of a plan (ws_scratch as for run_up).
+// built: fill *built with the launch of a Basic down GEMM instead of launching it.
 int run_down(const ffn_mi355x_plan* plan, const void* hidden, const void* w2, const void* b2, void* out, void* ws,
-             bool ws_scratch, void* hip_stream) {
+             bool ws_scratch, void* hip_stream, ffn::GemmParams* built = nullptr) {
     if (!valid_plan(plan)) return fail(FFN_MI355X_EINVAL, "invalid plan");
     if (!hidden || !w2 || !out) return fail(FFN_MI355X_EINVAL, "NULL device buffer");
     if (!aligned16(hidden) || !aligned16(w2) || !aligned16(out) || (ws && !aligned16(ws)) || (b2 && !aligned16(b2)))
@@ -660,7 +751,9 @@ int run_down(const ffn_mi355x_plan* plan, const void* hidden, const void* w2, co
         (b2 && (rc = check_span("bias2", b2, (size_t)plan->n * 2u)) != FFN_MI355X_OK) ||
         (rc = check_span("out", out, span_bytes(plan->mp, plan->np, plan->np))) != FFN_MI355X_OK ||
         (plan->down_impl == FFN_MI355X_DOWN_STREAMK && ws && !ws_scratch &&
-         (rc = check_span("ws", ws, plan->workspace_bytes)) != FFN_MI355X_OK))
+         (rc = check_span("ws", ws, plan->workspace_bytes)) != FFN_MI355X_OK) ||
+        (plan->down_impl != FFN_MI355X_DOWN_STREAMK && ws && !ws_scratch && up_counter_words(plan) > 0 &&
+         (rc = check_span("ws", ws, flags_bytes(plan))) != FFN_MI355X_OK))
         return rc;
     const Variant& D = kVariants[plan->down_variant];
     ffn::GemmParams gp;
@@ -680,6 +773,11 @@ int run_down(const ffn_mi355x_plan* plan, const void* hidden, const void* w2, co
     // more of hidden in the last-level cache (DiT-size FFN step: 1044 -> 1037 us Basic,
     // 1056 -> 1043 us Stream-K)
     gp.rev_m = 1;
+    if (ws && up_counter_words(plan) > 0) {
+        // the split up GEMM of the next call counts on zero counters: clear them here
+        gp.clear_words = up_counters(plan, ws);
+        gp.clear_count = (int)up_counter_words(plan);
+    }
     if (plan->down_impl == FFN_MI355X_DOWN_STREAMK) {
         if (!ws) return fail(FFN_MI355X_EINVAL, "Stream-K needs a workspace of %zu bytes", plan->workspace_bytes);
         const int G = plan->down_grid;
@@ -689,11 +787,41 @@ int run_down(const ffn_mi355x_plan* plan, const void* hidden, const void* w2, co
         gp.sk_q = (int)(total / G);
         gp.sk_r = (int)(total % G);
         gp.slots_per_wg = plan->down_slots_per_wg;
-        set_workspace(gp, plan, ws);
+        set_workspace(gp, plan, ws, false);
         return launch(D, plan->dtype, FFN_ROLE_DOWN_STREAMK, gp, G, hip_stream);
     }
     gp.dp_tiles = plan->down_tiles;
+    if (built) {
+        *built = gp;
+        return ok();
+    }
     return launch(D, plan->dtype, FFN_ROLE_DOWN_BASIC, gp, plan->down_grid, hip_stream);
+}
+
+// The whole FFN of a plan: one launch when the plan says so and X is not read as gathered rows
+// (ffn_fused.hip, counters in the workspace's counter region), else up then down.
+int run_ffn(const ffn_mi355x_plan* plan, const void* x, const void* w1, const void* b1, const void* w2,
+            const void* b2, void* hidden, void* out, void* ws, bool ws_scratch, void* hip_stream) {
+    if (!valid_plan(plan)) return fail(FFN_MI355X_EINVAL, "invalid plan");
+    int rc;
+    if (plan->single_launch && plan->x_d1 == 0) {
+        if (!ws) return fail(FFN_MI355X_EINVAL, "the single launch needs a workspace of %zu bytes", plan->workspace_bytes);
+        if (!ws_scratch && (rc = check_span("ws", ws, flags_bytes(plan))) != FFN_MI355X_OK) return rc;
+        ffn::GemmParams pu, pd;
+        int role = 0;
+        if ((rc = run_up(plan, x, w1, b1, hidden, nullptr, false, hip_stream, &pu, &role)) != FFN_MI355X_OK) return rc;
+        if ((rc = run_down(plan, hidden, w2, b2, out, nullptr, false, hip_stream, &pd)) != FFN_MI355X_OK) return rc;
+        const Variant& U = kVariants[plan->up_variant];
+        const Variant& D = kVariants[plan->down_variant];
+        ffn::FusedParams f;
+        f.ctr = (unsigned*)ws, f.ratio = U.bm / D.bm, f.spin_limit = 1 << 20;
+        const FusedPair* fp = fused_pair(plan->up_variant, plan->down_variant);
+        const hipError_t e = fp->launch[plan->dtype](role, &pu, &pd, &f, plan->block_num, (hipStream_t)hip_stream);
+        if (e != hipSuccess) return fail(FFN_MI355X_EHIP, "kernel launch failed: %s", hipGetErrorString(e));
+        return ok();
+    }
+    if ((rc = run_up(plan, x, w1, b1, hidden, ws, ws_scratch, hip_stream)) != FFN_MI355X_OK) return rc;
+    return run_down(plan, hidden, w2, b2, out, ws, ws_scratch, hip_stream);
 }
 
 // ---- scratch of the entry point that allocates nothing ----------------------------------
@@ -754,9 +882,7 @@ int ffn_mi355x_down(const ffn_mi355x_plan* plan, const void* hidden, const void*
 
 int ffn_mi355x_run(const ffn_mi355x_plan* plan, const void* x, const void* w1, const void* w2,
                    void* hidden, void* out, void* ws, void* hip_stream) {
-    int rc = run_up(plan, x, w1, nullptr, hidden, ws, false, hip_stream);
-    if (rc != FFN_MI355X_OK) return rc;
-    return run_down(plan, hidden, w2, nullptr, out, ws, false, hip_stream);
+    return run_ffn(plan, x, w1, nullptr, w2, nullptr, hidden, out, ws, false, hip_stream);
 }
 
 int ffn_mi355x_up_ex(const ffn_mi355x_plan* plan, const void* x, const void* w1, const void* b1, void* hidden,
@@ -773,9 +899,7 @@ int ffn_mi355x_run_ex(const ffn_mi355x_plan* plan, const void* x, const void* w1
                       const void* w2, const void* b2, void* hidden, void* out, void* ws, void* hip_stream) {
     if ((b1 == nullptr) != (b2 == nullptr))
         return fail(FFN_MI355X_EINVAL, "bias1 and bias2 are given together or not at all");
-    int rc = run_up(plan, x, w1, b1, hidden, ws, false, hip_stream);
-    if (rc != FFN_MI355X_OK) return rc;
-    return run_down(plan, hidden, w2, b2, out, ws, false, hip_stream);
+    return run_ffn(plan, x, w1, b1, w2, b2, hidden, out, ws, false, hip_stream);
 }
 
 int ffn_mi355x_run_noalloc(const ffn_mi355x_plan* plan, const void* x, const void* w1, const void* w2,
@@ -791,9 +915,7 @@ int ffn_mi355x_run_noalloc(const ffn_mi355x_plan* plan, const void* x, const voi
         const int rc = scratch_address(hip_stream, &ws);
         if (rc != FFN_MI355X_OK) return rc;
     }
-    int rc = run_up(plan, x, w1, nullptr, hidden, ws, true, hip_stream);
-    if (rc != FFN_MI355X_OK) return rc;
-    return run_down(plan, hidden, w2, nullptr, out, ws, true, hip_stream);
+    return run_ffn(plan, x, w1, nullptr, w2, nullptr, hidden, out, ws, true, hip_stream);
 }
 
 int ffn_mi355x_num_variants(void) { return kNumVariants; }

@@ -59,6 +59,12 @@
 
 #define FFN_NUM_VARIANTS 22
 
+// (up variant, down variant) pairs compiled as a single-launch FFN (ffn_fused.hip); the two tiles
+// of a pair have the same number of waves, and the up tile's rows are whole down tile rows.  The
+// aligned mid-size, unaligned and DiT-size FFNs' Basic tile pairs (the unaligned one's up on
+// variant 13, twelve-wave variant 18 having no eight-wave down to pair with).
+#define FFN_FUSED_PAIRS(X) X(12, 21) X(13, 19) X(12, 17)
+
 
 // launch roles of one variant
 // (the split up roles: tiles split along K, FP32 partials, the activation applied by the last

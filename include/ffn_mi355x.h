@@ -92,6 +92,12 @@ typedef struct ffn_mi355x_plan {
     /* Gathered rows of X (ffn_mi355x_set_x_rows): x_d1 = 0 reads row r at r * ldx; otherwise
        row r = (i0 * x_d1 + i1) * x_d2 + i2 starts at element i0*x_s0 + i1*x_s1 + i2*x_s2. */
     int x_d1, x_d2, x_s0, x_s1, x_s2;
+    /* 1: the FFN runs as one launch (up and down tiles in one persistent grid, a down tile
+       starting as soon as the hidden rows it reads are stored), where a single-launch kernel is
+       compiled for the tile pair (ffn_mi355x_set_single_launch; ffn_mi355x_make_plan leaves it
+       0, the two launches having measured faster); 0: two stream-ordered launches, up then
+       down. */
+    int single_launch;
     /* Check word over every field above, written by ffn_mi355x_make_plan and
        ffn_mi355x_set_operands.  The run entry points refuse a plan whose fields no longer
        match it (EINVAL "invalid plan"): its grids, tile counts and workspace size decide
@@ -138,15 +144,30 @@ int ffn_mi355x_set_operands(ffn_mi355x_plan* plan, int k, int h, int n, int ldx,
  * on a bad grid, plan unchanged. */
 int ffn_mi355x_set_x_rows(ffn_mi355x_plan* plan, int d1, int d2, int s0, int s1, int s2);
 
-/* Workspace bytes a plan needs (0 for the Basic down without a split up GEMM). */
+/* Turns the single launch of a plan on (1) or off (0).  On needs a compiled single-launch kernel
+ * for the plan's tile pair, a Basic down, an unsplit up GEMM with the GELU epilogue, at least
+ * eight up tile rows (one per XCD) and a K of at most 8192: ENOT_APPLICABLE otherwise.  A plan
+ * that can run as one launch holds at least the workspace's counter region in workspace_bytes
+ * either way, so its workspace serves both forms.  An X read as gathered rows
+ * (ffn_mi355x_set_x_rows) runs as two launches whatever the setting.  No counterpart in the
+ * reference, whose FFN is always one artifact (ops/api.py:43). */
+int ffn_mi355x_set_single_launch(ffn_mi355x_plan* plan, int on);
+
+/* Workspace bytes a plan needs (0 for the Basic down without a split up GEMM or a single
+ * launch). */
 int ffn_mi355x_workspace_bytes(const ffn_mi355x_plan* plan, size_t* bytes);
 
 /* Bytes at the start of every workspace that hold the split tiles' arrival counters (one
- * 32-bit counter per split tile and wave).  They must be zero before a workspace's first use
- * (e.g. allocate it zero-filled); every call leaves them zero again, so a workspace can serve
- * any plans whose workspace_bytes it covers, one call after another.  The rest of the
- * workspace needs no initialisation.  No counterpart in the reference, whose Stream-K reduction
- * is a separate phase (ops/kernel/ffn.py:1035-1175). */
+ * 32-bit counter per split tile and wave: the Stream-K down's from the start of the region, a
+ * split up GEMM's from its end).  Each GEMM's launch clears the other's counters before any
+ * tile, and every launch leaves its own zero: a Stream-K down therefore always starts from zero
+ * counters when its up GEMM ran first in the same call (ffn_mi355x_run, or ffn_mi355x_up given
+ * the workspace), whatever the region held, and a split up GEMM from its second call on.  Zero
+ * the region before the first call of a plan with a split up GEMM (e.g. allocate the workspace
+ * zero-filled).  A workspace can then serve any plans whose workspace_bytes it covers, one call
+ * after another; calls that overlap on one workspace race.  The rest of the workspace needs no
+ * initialisation.  No counterpart in the reference, whose Stream-K reduction is a separate
+ * phase (ops/kernel/ffn.py:1035-1175). */
 #define FFN_MI355X_WORKSPACE_COUNTER_BYTES (64u << 10)
 
 /* FFN_MI355X_WORKSPACE_COUNTER_BYTES when the plan needs a workspace, else 0. */
@@ -157,8 +178,8 @@ int ffn_mi355x_workspace_counter_bytes(const ffn_mi355x_plan* plan, size_t* byte
  * the single artifact(*tensors, block_num) launch of ops/api.py:43 built by
  * compile_kernel (ops/host/dispatch.py:97-116) from ops/kernel/ffn.py.
  * `ws` must hold plan->workspace_bytes whenever that is nonzero (Stream-K down or
- * split up), its counter bytes zero (ffn_mi355x_workspace_counter_bytes); it may be NULL
- * otherwise.
+ * split up), its counter bytes as FFN_MI355X_WORKSPACE_COUNTER_BYTES describes; it may be
+ * NULL otherwise.
  * The Stream-K down is one launch: the pieces of a split tile store FP32 partial tiles to `ws`,
  * and the last piece to arrive sums them in ascending K order, rounds once and stores the tile.
  * A split up is the same with the GELU applied after the sum. */

@@ -39,6 +39,11 @@ int ffn_mi355x_set_x_rows(ffn_mi355x_plan* plan, int d1, int d2, int s0, int s1,
     return FFN_MI355X_OK;
 }
 
+int ffn_mi355x_set_single_launch(ffn_mi355x_plan* plan, int on) {
+    plan->single_launch = 0;
+    return on ? FFN_MI355X_ENOT_APPLICABLE : FFN_MI355X_OK;
+}
+
 int ffn_mi355x_workspace_bytes(const ffn_mi355x_plan* plan, size_t* bytes) {
     *bytes = plan->workspace_bytes;
     return FFN_MI355X_OK;

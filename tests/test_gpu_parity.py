@@ -588,3 +588,108 @@ def test_streamk_finish_reproducible_and_resets(dtype):
         res = compare(outs[0].cpu(), golden)
         assert res["passed"] and res["mean_rel"] <= UNSTAGED_BOUND[dtype], (variant, block_num, res)
     assert 2 in pieces_seen and max(pieces_seen) >= 3   # tiles of two pieces and of three or more
+
+
+@pytest.mark.parametrize("fill", [0xFFFFFFFF, 7, "random"])
+def test_dirty_counter_region_is_repaired(fill):
+    """The workspace's arrival counters need not start at zero for a Stream-K down after its up
+    GEMM: the up launch clears them.  A counter region filled with garbage (all ones, a small
+    count, random words) gives the same output, bit for bit, as a zeroed one, and the counter words
+    the plan uses are left zero.
+    A split up GEMM's counters are cleared by the down launch: after one down call on a dirty
+    region the whole FFN (decode shard, split up) is right again."""
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    gen = torch.Generator().manual_seed(23)
+
+    def dirty(ws, plan):
+        n = _lib.workspace_counter_bytes(plan) // 4
+        words = ws[:n].view(torch.int32)
+        if fill == "random":
+            words.copy_(torch.randint(-2 ** 31, 2 ** 31 - 1, (n,), generator=gen, dtype=torch.int32))
+        else:
+            words.fill_(fill - 2 ** 32 if fill >= 2 ** 31 else fill)
+
+    def used_counters_zero(plan, ws):
+        """The counter words this plan's two GEMMs use (the down's from the start of the region,
+        a split up's from its end) are zero; the plan does not touch the others."""
+        info = _lib.variants()
+        words = ws[:_lib.workspace_counter_bytes(plan) // 4].view(torch.int32)
+        tile_waves = lambda v: info[v]["waves"] - info[v]["refill_waves"]
+        down = plan.down_sk_tiles * tile_waves(plan.down_variant) if plan.down_impl == 1 else 0
+        up = plan.up_sk_tiles * tile_waves(plan.up_variant)
+        return not bool(words[:down].any()) and not bool(words[words.numel() - up:].any())
+
+    def run(plan, x, w1, w2, ws):
+        hid = torch.empty((plan.mp, plan.hp), dtype=x.dtype, device="cuda")
+        out = torch.full((plan.mp, plan.np), float("nan"), dtype=x.dtype, device="cuda")
+        _lib.check(lib.ffn_mi355x_run(ctypes.byref(plan), x.data_ptr(), w1.data_ptr(), w2.data_ptr(),
+                                      hid.data_ptr(), out.data_ptr(), ws.data_ptr(), stream))
+        torch.cuda.synchronize()
+        return out
+
+    # Stream-K down with an unsplit up (tiles of two and more pieces at 37 workgroups)
+    mp, kp, hp, np_ = 320, 256, 2048, 448
+    x = torch.randn(mp, kp, generator=gen).to(torch.bfloat16).cuda()
+    w1 = (torch.randn(hp, kp, generator=gen) * kp ** -0.5).to(torch.bfloat16).cuda()
+    w2 = (torch.randn(np_, hp, generator=gen) * hp ** -0.5).to(torch.bfloat16).cuda()
+    plan = _plan(mp, kp, hp, np_, torch.bfloat16, "streamk", 37)
+    assert plan.down_sk_tiles > 0 and plan.up_sk_tiles == 0
+    clean = torch.zeros(plan.workspace_bytes // 4, dtype=torch.float32, device="cuda")
+    want = run(plan, x, w1, w2, clean)
+    ws = torch.zeros_like(clean)
+    dirty(ws, plan)
+    got = run(plan, x, w1, w2, ws)
+    say("dirty counters, stream-k down", fill, plan.down_sk_tiles)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    assert used_counters_zero(plan, ws)
+
+    # split up GEMM (decode shard: 16 x 5120 -> 1728 -> 5120): one down call repairs its counters
+    case = get_case("c4_tp8_shard_bf16")
+    x, w1, w2 = make_inputs(case, "cuda")
+    m, k = x.numel() // x.shape[-1], x.shape[-1]
+    plan = _lib.make_plan(64, k, w1.shape[0], w2.shape[0], _lib.BF16, "basic", "erf", 256, m=m)
+    assert plan.up_sk_tiles > 0
+    xp = torch.zeros((64, k), dtype=x.dtype, device="cuda")
+    xp[:m] = x.reshape(m, k)
+    clean = torch.zeros(plan.workspace_bytes // 4, dtype=torch.float32, device="cuda")
+    want = run(plan, xp, w1, w2, clean)
+    ws = torch.zeros_like(clean)
+    dirty(ws, plan)
+    hid = torch.zeros((plan.mp, plan.hp), dtype=x.dtype, device="cuda")
+    out = torch.empty((plan.mp, plan.np), dtype=x.dtype, device="cuda")
+    _lib.check(lib.ffn_mi355x_down(ctypes.byref(plan), hid.data_ptr(), w2.data_ptr(), out.data_ptr(),
+                                   ws.data_ptr(), stream))
+    got = run(plan, xp, w1, w2, ws)
+    say("dirty counters, split up", fill, plan.up_sk_tiles)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    assert used_counters_zero(plan, ws)
+
+
+@pytest.mark.parametrize("case_id,upv,downv", [("c2_aligned_bf16", 12, 21), ("c3_unaligned_fp16", 13, 19),
+                                              ("c5_dit_bf16", 12, 17)])
+def test_single_launch_matches_two_launches(case_id, upv, downv):
+    """The FFN as one launch (up and down tiles in one persistent grid, per-XCD queues, down tiles
+    waiting on per-row-block counters) computes every tile as the two launches do: the outputs
+    are bit-identical, over three calls in a row, the queues and counters are left zero and no
+    down tile gave up waiting.  The first case also meets the reference criterion against the
+    oracle."""
+    case = get_case(case_id)
+    x, w1, w2 = make_inputs(case, "cuda")
+    say("single launch", case_id, upv, downv, "two launches")
+    two = prepare_ffn(x, w1, w2, up_variant=upv, down_variant=downv, single_launch=False)
+    want = two.run().clone()
+    torch.cuda.synchronize()
+    say("single launch", case_id, upv, downv, "one launch")
+    one = prepare_ffn(x, w1, w2, up_variant=upv, down_variant=downv, single_launch=True)
+    assert one.plan.native.single_launch == 1 and two.plan.native.single_launch == 0
+    ws = one.storage[5]
+    for call in range(3):
+        got = one.run()
+        torch.cuda.synchronize()
+        say("single launch", case_id, "call", call)
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), (case_id, call)
+        words = ws.view(torch.int32)[:_lib.workspace_counter_bytes(one.plan.native) // 4]
+        assert not bool(words.any()), words.nonzero()[:8]   # error word included
+    if case_id == "c2_aligned_bf16":
+        assert_parity(got, x, w1, w2, tag="single launch c2")

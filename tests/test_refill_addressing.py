@@ -214,3 +214,43 @@ def test_single_launch_schedule_of_the_faulting_run(every_wave):
         # the last up tile row (row-block 15, XCD 7) and every tile of the last column
         assert {(p[0], p[2]) for p in past if p[4] == "x"} == {(7, 15)}
         assert {p[3] for p in past if p[4] == "w1"} == {tiles_n_up - 1}
+
+
+FUSED_PAIRS = [tuple(int(v) for v in pair) for pair in re.findall(
+    r"X\((\d+),\s*(\d+)\)", re.search(r"^#define FFN_FUSED_PAIRS\(X\)(.*)$", VARIANTS.read_text(), re.M).group(1))]
+
+
+@pytest.mark.parametrize("pair,shape", [
+    ((12, 21), (4096, 4096, 1024, 4096, 1024)),      # aligned mid-size: (m, mp, k, h, n)
+    ((13, 19), (1005, 1024, 1008, 3008, 1024)),      # unaligned, padded buffers
+    ((12, 17), (8192, 8192, 3072, 12288, 3072)),     # DiT-size
+])
+def test_single_launch_pairs_stay_inside_their_operands(pair, shape):
+    """The compiled single-launch pairs (ffn_fused.hip) on the workloads they serve: both tiles
+    have the same number of waves, the up tile's rows hold whole down tile rows, every XCD owns
+    an up row block, every tile is handed out once, and with the kernels' role split every
+    SALU-addressed refill of an interior tile (the others take the range-checked refill) stays
+    inside its operand."""
+    assert pair in FUSED_PAIRS
+    up, dn = TILES[pair[0]], TILES[pair[1]]
+    m, mp, k, h, n = shape
+    assert up.nw + up.prod == dn.nw + dn.prod and up.bm % dn.bm == 0
+    tiles_m_up, tiles_n_up = -(-m // up.bm), -(-h // up.bn)
+    tiles_m_dn, tiles_n_dn = -(-m // dn.bm), -(-n // dn.bn)
+    assert tiles_m_up >= 8
+    tickets = list(fused_tickets(tiles_m_up, tiles_n_up, tiles_m_dn, tiles_n_dn, up.bm // dn.bm))
+    assert sorted((ph, a, b) for _, ph, a, b in tickets) == sorted(
+        [("up", a, b) for a in range(tiles_m_up) for b in range(tiles_n_up)]
+        + [("down", a, b) for a in range(tiles_m_dn) for b in range(tiles_n_dn)])
+    # a down tile's rows lie in an up row block of its own XCD
+    for x, phase, tm, _ in tickets:
+        if phase == "down":
+            assert (tm * dn.bm // up.bm) % 8 == x
+    sizes = {"x": mp * k * 2, "w1": h * k * 2, "hidden": mp * h * 2, "w2": n * h * 2}
+    for x, phase, tm, tn in tickets:
+        t, rows, cols, depth, a_name, b_name = ((up, m, h, k, "x", "w1") if phase == "up"
+                                                else (dn, m, n, h, "hidden", "w2"))
+        if (tm + 1) * t.bm > rows or (tn + 1) * t.bn > cols:
+            continue   # edge tile: range-checked refill
+        a_end, b_end = refill_span(t, tm, tn, depth, mp, depth, cols, depth, every_wave=False)
+        assert a_end <= sizes[a_name] and b_end <= sizes[b_name], (phase, tm, tn)
