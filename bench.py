@@ -214,9 +214,11 @@ COPY_BYTES = 512 << 20   # calibration copy: reads and writes exactly this many 
 def counters_pass(case):
     """Launch sequence for a counter run: the calibration copy (torch's elementwise copy kernel
     over COPY_BYTES, so FETCH_SIZE/WRITE_SIZE of a kernel with known traffic can be read off),
-    then up and down of both down paths, three times each, untimed."""
+    then up and down of both down paths, three times each, then torch's unfused path three
+    times (the library comparison), all untimed."""
     import ctypes
     import torch
+    import torch.nn.functional as F
     from ffn_optim_amd import _lib, prepare_ffn
     from ffn_optim_amd.cases import make_inputs
     src = torch.ones(COPY_BYTES // 4, device="cuda", dtype=torch.float32)
@@ -241,6 +243,13 @@ def counters_pass(case):
         torch.cuda.synchronize()
         print(f"counters pass: {case['case_id']} {down} up v{plan.up_variant} down v{plan.down_variant}",
               flush=True)
+    # torch's unfused path on the same inputs (hipBLASLt GEMM, elementwise GELU, hipBLASLt GEMM),
+    # three times, for the library comparison
+    x2 = x.reshape(-1, x.shape[-1])
+    for _ in range(3):
+        F.gelu(x2 @ w1.t()) @ w2.t()
+    torch.cuda.synchronize()
+    print(f"counters pass: {case['case_id']} torch unfused", flush=True)
 
 
 def cold_step_time(case, down, steps, inputs):
