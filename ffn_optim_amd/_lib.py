@@ -21,6 +21,9 @@ ACTIVATION_CODES = {"gelu:erf": 0, "gelu:rational": 1, "silu": 2, "swiglu": 3}
 OK, EINVAL, ENOT_APPLICABLE, EUNAVAILABLE, EHIP, EDEVICE = 0, -1, -2, -3, -4, -5
 # FFN_MI355X_MAX_PITCH: the largest operand row pitch (elements) ffn_mi355x_set_operands accepts
 MAX_PITCH = 4_000_000
+# FFN_MI355X_SPLIT_COUNTER_WORDS: words from one split tile's arrival counters to the next, when
+# both GEMMs' split tiles fit the counter region that way (else one word per tile wave)
+SPLIT_COUNTER_WORDS = 32
 
 
 class PlanStruct(ctypes.Structure):

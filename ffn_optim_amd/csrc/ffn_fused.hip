@@ -118,7 +118,7 @@ __global__ void __launch_bounds__(CU::NT) ffn_fused_kernel(GemmParams pu, GemmPa
     while (true) {
         wait_vmcnt<0>();
         __syncthreads();
-        if (threadIdx.x == 0) *ticket = (int)__hip_atomic_fetch_add(f.ctr + x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (threadIdx.x == 0) *ticket = (int)__hip_atomic_fetch_add(f.ctr + x * kFusedStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
         const int t = __builtin_amdgcn_readfirstlane(*ticket);
         __syncthreads();  // every wave has read the ticket before stage 0 is refilled
@@ -132,7 +132,7 @@ __global__ void __launch_bounds__(CU::NT) ffn_fused_kernel(GemmParams pu, GemmPa
             wait_vmcnt<0>();
             __syncthreads();
             if (threadIdx.x == 0)
-                __hip_atomic_fetch_add(f.ctr + kFusedReady + rb, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_fetch_add(f.ctr + kFusedReady + rb * kFusedStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         } else if (t < n_up + n_down) {
             int j = t - n_up, rb = x;
             for (int i = 0; i < nrb; ++i) {
@@ -144,12 +144,12 @@ __global__ void __launch_bounds__(CU::NT) ffn_fused_kernel(GemmParams pu, GemmPa
             if (threadIdx.x == 0) {
                 const unsigned need = (unsigned)pu.tiles_n;
                 int polls = 0;
-                while (__hip_atomic_load(f.ctr + kFusedReady + rb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
+                while (__hip_atomic_load(f.ctr + kFusedReady + rb * kFusedStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
                     if (++polls > f.spin_limit) {
                         __hip_atomic_store(f.ctr + kFusedError, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                         break;
                     }
-                    __builtin_amdgcn_s_sleep(2);
+                    __builtin_amdgcn_s_sleep(4);
                 }
             }
             __syncthreads();
@@ -166,9 +166,9 @@ __global__ void __launch_bounds__(CU::NT) ffn_fused_kernel(GemmParams pu, GemmPa
     if (threadIdx.x == 0) {
         const unsigned left = __hip_atomic_fetch_add(f.ctr + kFusedLeft, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (left == (unsigned)G - 1) {
-            for (int i = 0; i < 8; ++i) __hip_atomic_store(f.ctr + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int i = 0; i < 8; ++i) __hip_atomic_store(f.ctr + i * kFusedStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             for (int i = 0; i < pu.tiles_m; ++i)
-                __hip_atomic_store(f.ctr + kFusedReady + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(f.ctr + kFusedReady + i * kFusedStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(f.ctr + kFusedLeft, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }

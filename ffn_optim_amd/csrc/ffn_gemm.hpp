@@ -51,6 +51,7 @@ struct GemmParams {
     void* c;              // [M][ldc]   hidden or out
     float* ws;            // Stream-K partial-tile slots (FP32), ws_bytes long
     unsigned* sk_flags;   // per split tile and wave: arrivals of the tile's pieces (zero between launches)
+    int sk_stride;        // words from one split tile's counters to the next's (at least the tile waves)
     unsigned ws_bytes;
     int M, N, K;
     int m_valid;          // rows of A holding data; rows [m_valid, M) are zero padding
@@ -83,17 +84,22 @@ struct GemmParams {
 };
 
 // Counter words of a single-launch FFN (ffn_fused.hip), in the workspace's counter region; zero
-// between launches (the last workgroup to leave clears them) but for the error word:
-//   [0, 8)             ticket queue of each XCD
-//   [8]                workgroups that have left
-//   [9]                error word: set when a down tile gave up waiting for its row block
-//   [16, 16 + R)       up tiles stored, per up row block
+// between launches (the last workgroup to leave clears them) but for the error word.  Each
+// counter has a 256-byte line of its own (kFusedStride words): atomics on one line are
+// serialised, ~11 ns apiece, so with every workgroup's tickets, arrivals and polls on a single
+// line each ticket waited ~3 us (256 workgroups, one fetch-add each, measured), against ~0.35 us
+// on lines of their own.
+//   x * S              ticket queue of XCD x (x < 8)
+//   8 * S              workgroups that have left
+//   9 * S              error word: set when a down tile gave up waiting for its row block
+//   (10 + r) * S       up tiles stored, of up row block r
+constexpr int kFusedStride = 64;
+constexpr int kFusedLeft = 8 * kFusedStride, kFusedError = 9 * kFusedStride, kFusedReady = 10 * kFusedStride;
 struct FusedParams {
     unsigned* ctr;
     int ratio;       // down row blocks per up row block (BM_up / BM_down)
     int spin_limit;  // polls of a row-block counter before a down tile gives up
 };
-constexpr int kFusedLeft = 8, kFusedError = 9, kFusedReady = 16;
 
 // SYNCQ_: MFMA slot of a stage's last k-step after which the stage wait + barrier is placed
 // (-1: end of the first block of B).  DMAKS_: with two stages, the k-steps at the start of an
@@ -1195,7 +1201,9 @@ struct Engine {
         const int kI = p.k_iters, sp = u.split;
         const int first = sk_owner(p, sp * kI), last = sk_owner(p, sp * kI + kI - 1);
         wait_vmcnt<0>();
-        unsigned* flag = p.sk_flags + (size_t)sp * C::NW + twave;
+        // (sk_stride: 32 words, one 128-byte line per split tile, or NW when packed)
+        static_assert(C::NW <= 32, "a split tile's counters fit one 128-byte line");
+        unsigned* flag = p.sk_flags + (size_t)sp * (size_t)p.sk_stride + twave;
         unsigned old = 0;
         if (lane == 0) old = __hip_atomic_fetch_add(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         old = (unsigned)__builtin_amdgcn_readfirstlane((int)old);

@@ -402,11 +402,26 @@ size_t flags_bytes(const ffn_mi355x_plan*) { return kCounterBytes; }
 // Arrival counters (one word per split tile and wave): the Stream-K down's from the start of the
 // counter region, a split up GEMM's from its end, so that each GEMM's launch can clear the
 // other's (GemmParams::clear_words) without touching its own.
+// Each split tile's counters take a 128-byte line of their own (FFN_MI355X_SPLIT_COUNTER_WORDS
+// words) when both GEMMs' split tiles fit the region that way, else they are packed (the tile's
+// waves only).  Atomics on one line are serialised (~11 ns apiece), and every piece of every
+// split tile counts in at about the same time, at the end of a launch: packed, the decode FFN's
+// Stream-K down put 96 arrivals (8 tiles x 3 pieces x 4 waves) on each line.
+constexpr int kSplitWords = FFN_MI355X_SPLIT_COUNTER_WORDS;
+bool spread_counters(long long up_sk, long long down_sk) {
+    return (up_sk + down_sk) * kSplitWords <= (long long)(kCounterBytes / 4);
+}
+long long down_split_tiles(const ffn_mi355x_plan* p) {
+    return p->down_impl == FFN_MI355X_DOWN_STREAMK ? p->down_sk_tiles : 0;
+}
+int counter_stride(const ffn_mi355x_plan* p, const Variant& v) {
+    return spread_counters(p->up_sk_tiles, down_split_tiles(p)) ? kSplitWords : v.nw;
+}
 size_t down_counter_words(const ffn_mi355x_plan* p) {
-    return p->down_impl == FFN_MI355X_DOWN_STREAMK ? (size_t)p->down_sk_tiles * kVariants[p->down_variant].nw : 0;
+    return (size_t)down_split_tiles(p) * (size_t)counter_stride(p, kVariants[p->down_variant]);
 }
 size_t up_counter_words(const ffn_mi355x_plan* p) {
-    return p->up_sk_tiles > 0 ? (size_t)p->up_sk_tiles * kVariants[p->up_variant].nw : 0;
+    return p->up_sk_tiles > 0 ? (size_t)p->up_sk_tiles * (size_t)counter_stride(p, kVariants[p->up_variant]) : 0;
 }
 unsigned* up_counters(const ffn_mi355x_plan* p, void* ws) {
     return (unsigned*)ws + (kCounterBytes / 4 - up_counter_words(p));
@@ -425,7 +440,7 @@ bool fused_ok(const ffn_mi355x_plan* p) {
     return p->down_impl == FFN_MI355X_DOWN_BASIC && p->up_sk_tiles == 0 &&
            (p->activation == FFN_MI355X_GELU_ERF || p->activation == FFN_MI355X_GELU_RATIONAL) &&
            U.nw + U.prod == D.nw + D.prod && U.bm % D.bm == 0 && rbs >= 8 &&
-           ffn::kFusedReady + rbs <= (long long)(kCounterBytes / 4) && fast_dma_for(p->kp);
+           ffn::kFusedReady + rbs * ffn::kFusedStride <= (long long)(kCounterBytes / 4) && fast_dma_for(p->kp);
 }
 
 int launch(const Variant& v, int dtype, int role, const ffn::GemmParams& gp, int grid,
@@ -650,6 +665,7 @@ namespace {
 void set_workspace(ffn::GemmParams& gp, const ffn_mi355x_plan* plan, void* ws, bool up) {
     const size_t f = flags_bytes(plan);
     gp.sk_flags = up ? up_counters(plan, ws) : (unsigned*)ws;
+    gp.sk_stride = counter_stride(plan, kVariants[up ? plan->up_variant : plan->down_variant]);
     gp.ws = (float*)((char*)ws + f);
     gp.ws_bytes = (unsigned)(plan->workspace_bytes - f);
 }

@@ -159,7 +159,9 @@ int ffn_mi355x_workspace_bytes(const ffn_mi355x_plan* plan, size_t* bytes);
 
 /* Bytes at the start of every workspace that hold the split tiles' arrival counters (one
  * 32-bit counter per split tile and wave: the Stream-K down's from the start of the region, a
- * split up GEMM's from its end).  Each GEMM's launch clears the other's counters before any
+ * split up GEMM's from its end; each split tile's counters start FFN_MI355X_SPLIT_COUNTER_WORDS
+ * words after the previous tile's when both GEMMs' split tiles fit the region that way, else
+ * they are packed, one word per wave of the tile).  Each GEMM's launch clears the other's counters before any
  * tile, and every launch leaves its own zero: a Stream-K down therefore always starts from zero
  * counters when its up GEMM ran first in the same call (ffn_mi355x_run, or ffn_mi355x_up given
  * the workspace), whatever the region held, and a split up GEMM from its second call on.  Zero
@@ -169,6 +171,8 @@ int ffn_mi355x_workspace_bytes(const ffn_mi355x_plan* plan, size_t* bytes);
  * initialisation.  No counterpart in the reference, whose Stream-K reduction is a separate
  * phase (ops/kernel/ffn.py:1035-1175). */
 #define FFN_MI355X_WORKSPACE_COUNTER_BYTES (64u << 10)
+/* Words from one split tile's arrival counters to the next (a 128-byte line each). */
+#define FFN_MI355X_SPLIT_COUNTER_WORDS 32
 
 /* FFN_MI355X_WORKSPACE_COUNTER_BYTES when the plan needs a workspace, else 0. */
 int ffn_mi355x_workspace_counter_bytes(const ffn_mi355x_plan* plan, size_t* bytes);

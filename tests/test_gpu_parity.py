@@ -616,8 +616,11 @@ def test_dirty_counter_region_is_repaired(fill):
         info = _lib.variants()
         words = ws[:_lib.workspace_counter_bytes(plan) // 4].view(torch.int32)
         tile_waves = lambda v: info[v]["waves"] - info[v]["refill_waves"]
-        down = plan.down_sk_tiles * tile_waves(plan.down_variant) if plan.down_impl == 1 else 0
-        up = plan.up_sk_tiles * tile_waves(plan.up_variant)
+        down_sk = plan.down_sk_tiles if plan.down_impl == 1 else 0
+        spread = (down_sk + plan.up_sk_tiles) * _lib.SPLIT_COUNTER_WORDS <= words.numel()
+        stride = lambda v: _lib.SPLIT_COUNTER_WORDS if spread else tile_waves(v)
+        down = down_sk * stride(plan.down_variant)
+        up = plan.up_sk_tiles * stride(plan.up_variant)
         return not bool(words[:down].any()) and not bool(words[words.numel() - up:].any())
 
     def run(plan, x, w1, w2, ws):

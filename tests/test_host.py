@@ -636,3 +636,14 @@ def test_tuned_table_assignments(case_id, down):
     from ffn_optim_amd.cases import get_case
     plan = make_plan(case_problem(get_case(case_id)), Selection("basic", down), 256)
     assert (plan.up.variant, plan.down.variant) == TUNED_ASSIGNMENTS[(case_id, down)]
+
+
+def test_split_counter_stride_matches_header():
+    """The Python mirror of the arrival-counter layout (used by the GPU tests that check which
+    counter words a plan leaves zero) is the header's FFN_MI355X_SPLIT_COUNTER_WORDS, a 128-byte
+    line of 32-bit counters that holds every tile wave of the widest tile."""
+    header = (Path(__file__).resolve().parent.parent / "include" / "ffn_mi355x.h").read_text()
+    words = int(re.search(r"#define FFN_MI355X_SPLIT_COUNTER_WORDS (\d+)", header).group(1))
+    assert words == _lib.SPLIT_COUNTER_WORDS == 32
+    info = _lib.variants()
+    assert max(v["waves"] - v["refill_waves"] for v in info) <= words
