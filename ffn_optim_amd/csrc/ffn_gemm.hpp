@@ -108,7 +108,7 @@ struct FusedParams {
 // WTM x WTN wave tile over its own BK/WGK slice of every stage, and the WGK partial tiles are
 // summed through LDS after the main loop.
 template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int STAGES_, int SYNCQ_ = -1, int DMAKS_ = -1,
-          int WGK_ = 1, int DMAW_ = 0, int PROD_ = 0>
+          int WGK_ = 1, int DMAW_ = 0, int PROD_ = 0, int EARLY_ = 0>
 struct TileCfg {
     static constexpr int BM = BM_, BN = BN_, BK = BK_;
     static constexpr int WGM = WGM_, WGN = WGN_, WGK = WGK_, STAGES = STAGES_;
@@ -139,6 +139,12 @@ struct TileCfg {
     static_assert(PROD == 0 || DMAW_ == 0, "refill-only waves issue the whole refill");
     static constexpr int A_PW = A_BLKS / DW, B_PW = B_BLKS / DW;  // DMA blocks per issuing wave
     static constexpr int LOADS = A_PW + B_PW;      // DMA instructions per issuing wave per stage
+    // EARLY_ > 0 (two stages only): the first EARLY_ of an iteration's LOADS go out in the slots
+    // after the previous iteration's stage barrier -- the moment the stage they fill is free --
+    // instead of in the iteration before the data is used: a full iteration of lead for them.
+    static constexpr int EARLY = EARLY_;
+    static_assert(EARLY_ == 0 || (STAGES_ == 2 && WGK_ == 1 && EARLY_ < A_PW + B_PW),
+                  "early refill: two stages, no K slices, part of the refill");
     static constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
     static constexpr int KSTEPS = BK / 16 / WGK;   // MFMA k-steps per stage and wave
     // Output staging of the epilogue: from stage STAGES-1 (which the next unit's DMA prologue
@@ -517,9 +523,11 @@ struct Engine {
     struct DmaIt {
         uint32_t k0x2;
         int lim;
+        uint32_t e_k0x2;  // the same for the iteration whose early refill (C::EARLY) this one issues
+        int e_lim;
     };
     __device__ __forceinline__ DmaIt dma_it(const GemmParams& p, int kit, bool real) const {
-        DmaIt t;
+        DmaIt t{};
         t.k0x2 = (uint32_t)(kit * C::BK * 2);
         t.lim = real ? p.K - kit * C::BK : 0;
         return t;
@@ -616,7 +624,12 @@ struct Engine {
 #pragma unroll
         for (int s = 0; s < S - 1; ++s)
             issue_range<false, 0, C::LOADS>(p, ra, rb, s, L, dma_it(p, u.kb + s, u.kb + s < u.ke));
+        // the early part of iteration S-1, whose stage is free too
+        if constexpr (C::EARLY > 0)
+            issue_range<false, 0, C::EARLY>(p, ra, rb, S - 1, L, dma_it(p, u.kb + S - 1, u.kb + S - 1 < u.ke));
     }
+    // loads of an issuing wave's DMA prologue (what the next unit has in flight at its start)
+    static constexpr int PRO_LOADS = C::LOADS * (S - 1) + C::EARLY;
 
     // Fragment registers: A (activation rows) double-buffered across k-steps, B (weight rows)
     // reloaded in place right after its last use, which the j-major MFMA order makes early.
@@ -738,11 +751,19 @@ struct Engine {
                 // B fragment jj is reloaded once both its last use (the end of block jj) and
                 // the barrier are behind
                 reload_b_at<Q, 0>(nxt);
+                // the stage this iteration read is free: the early part of the iteration after
+                // next goes into it (range-checked: that iteration may be a K tail or past the
+                // unit, which reads zeros)
+                if constexpr (C::EARLY > 0 && DMA) {
+                    constexpr int e0 = qq * C::EARLY / span, e1 = (qq + 1) * C::EARLY / span;
+                    issue_range<false, e0, e1>(p, ra, rb, cur, L, DmaIt{o.e_k0x2, o.e_lim, 0u, 0});
+                }
             }
         }
-        constexpr int g = KSI * NM + Q;  // this slot's share of the refill DMA
+        constexpr int g = KSI * NM + Q;  // this slot's share of the refill DMA (the loads past the early part)
         if constexpr (DMA && g < DMA_SLOTS && (DMA_ALL || KSI + 1 < KS || Q < SYNC_Q)) {
-            constexpr int t0 = g * C::LOADS / DMA_SLOTS, t1 = (g + 1) * C::LOADS / DMA_SLOTS;
+            constexpr int t0 = C::EARLY + g * (C::LOADS - C::EARLY) / DMA_SLOTS;
+            constexpr int t1 = C::EARLY + (g + 1) * (C::LOADS - C::EARLY) / DMA_SLOTS;
             issue_range<FAST, t0, t1>(p, ra, rb, dma_stage, L, o);
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -780,7 +801,11 @@ struct Engine {
                                          const __amdgpu_buffer_rsrc_t& ra, const __amdgpu_buffer_rsrc_t& rb,
                                          const DmaLane& L, f32x16 (&acc)[FN][FM], int& cur, int it, int n) {
         const int dkit = it + S - 1;
-        const DmaIt o = dma_it(p, u.kb + dkit, FAST || dkit < n);
+        DmaIt o = dma_it(p, u.kb + dkit, FAST || dkit < n);
+        if constexpr (C::EARLY > 0) {
+            const DmaIt e = dma_it(p, u.kb + dkit + 1, dkit + 1 < n);
+            o.e_k0x2 = e.k0x2, o.e_lim = e.lim;
+        }
         const int dstage = (cur == 0) ? S - 1 : cur - 1;
         ksteps<FAST, false, 0>(p, nx, ra, rb, cur, dstage, L, o, acc);
         cur = (cur + 1 == S) ? 0 : cur + 1;
@@ -809,7 +834,7 @@ struct Engine {
         rsrc(p, u, ra, rb);
         const DmaLane L = dma_lane(p, u);
         const int n = u.ke - u.kb;
-        if (first) wait_vmcnt<C::LOADS * (S - 2)>();
+        if (first) wait_vmcnt<C::LOADS * (S - 2) + C::EARLY>();
         else wait_vmcnt<0>();
         barrier();
         read_a_range<0, 0, FM>(0, 0);
@@ -825,7 +850,7 @@ struct Engine {
             for (; it < fast_end && it < n - 1; ++it) step<true>(p, u, nx, ra, rb, L, acc, cur, it, n);
         }
         for (; it < n - 1; ++it) step<false>(p, u, nx, ra, rb, L, acc, cur, it, n);
-        ksteps<false, true, 0>(p, nx, ra, rb, cur, 0, L, DmaIt{0u, 0}, acc);
+        ksteps<false, true, 0>(p, nx, ra, rb, cur, 0, L, DmaIt{0u, 0, 0u, 0}, acc);
     }
 
     // ---- epilogue through LDS --------------------------------------------------------------
@@ -884,10 +909,11 @@ struct Engine {
                                                       f32x16 (&acc)[FN][FM]) {
         static_assert(C::OUT_POW2, "the staging swizzle needs a power-of-two number of pieces per row");
         static_assert((ER * TPR) % NT == 0, "chunk pieces split evenly over the threads");
+        static_assert(C::EARLY == 0, "the next unit's early refill fills part of the staging stage");
         lds_char* eb = smem + C::EPI_OFF;
         // DMA still in flight may target any stage but the next unit's prologue (issued last):
         // drain it; the barrier before the first staging write makes sure every wave has
-        if (next) wait_vmcnt<C::LOADS * (S - 1)>();
+        if (next) wait_vmcnt<PRO_LOADS>();
         else wait_vmcnt<0>();
         const int row0 = u.tm * C::BM, col0 = u.tn * C::BN;
         // opaque copies: the addressing below depends only on the thread id, and would
@@ -1101,7 +1127,7 @@ struct Engine {
                                                     f32x16 (&acc)[FN][FM]) {
         // DMA still in flight may target any stage but the next unit's prologue (issued last):
         // drain it; the barrier makes sure every wave has before the area is written
-        if (next) wait_vmcnt<C::LOADS * (S - 1)>();
+        if (next) wait_vmcnt<PRO_LOADS>();
         else wait_vmcnt<0>();
         barrier();
         xphases<WK, 0>(acc);
@@ -1118,7 +1144,7 @@ struct Engine {
         }
     }
     __device__ __forceinline__ void store_sliced_sync(bool next) const {
-        if (next) wait_vmcnt<C::LOADS * (S - 1)>();
+        if (next) wait_vmcnt<PRO_LOADS>();
         else wait_vmcnt<0>();
         barrier();
         xphase_barriers<0>();
@@ -1239,7 +1265,7 @@ struct Engine {
     template <int EPI, int WK>
     __device__ __forceinline__ void finish_piece_sliced_as(const GemmParams& p, const Unit& u, int v,
                                                            uint32_t slot_off, bool next, f32x16 (&acc)[FN][FM]) {
-        if (next) wait_vmcnt<C::LOADS * (S - 1)>();
+        if (next) wait_vmcnt<PRO_LOADS>();
         else wait_vmcnt<0>();
         barrier();
         xphases<WK, 0>(acc);
@@ -1276,8 +1302,10 @@ struct Engine {
 // registers; its Stream-K pieces exchange first and then store their FP32 partials.  A tile
 // whose output rows are not a power-of-two number of 16-byte pieces stores from registers, and
 // so does a tile with refill-only waves: they skip the epilogue, which may then hold no barrier.
+// A tile with an early refill stores from registers too: the next unit's DMA prologue then fills
+// part of stage S-1, the staging area.
 template <class C, int EPI, bool SK>
-constexpr bool epi_in_regs() { return EPI != EPI_STORE || SK || !C::OUT_POW2 || C::PROD > 0; }
+constexpr bool epi_in_regs() { return EPI != EPI_STORE || SK || !C::OUT_POW2 || C::PROD > 0 || C::EARLY > 0; }
 
 // The wave roles of a tile: with refill-only waves (C::PROD > 0) waves [0, PROD) issue the whole
 // refill and hold no wave tile, and the others hold wave tiles and issue no DMA; otherwise every
