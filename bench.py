@@ -7,7 +7,12 @@ workload is the largest configuration, the DiT-style FFN (X [2,4096,3072] bf16,
 W1 [12288,3072], W2 [3072,12288]), on which the 60%-of-MFMA-peak target is
 stated; the other workloads are reported beside it.  ms_per_step follows
 performance/collect.py:8-35 of the reference: warmup, then one device event pair
-around every run(), median.  The mean of the same steps issued back to back under
+around every run(), median; the K timed runs of the Basic path, the Stream-K path
+and torch's unfused path are taken in alternating rounds (time_interleaved), so
+that all three see the same stretch of the GPU's power and thermal state
+(memory-bound workloads path by path, each warm time with its own weights in the
+last-level cache; their cold times are timed apart).  The
+mean of the same steps issued back to back under
 one event pair is reported beside it (it leaves out the host's per-call launch
 gap).  Each path also reports max_abs, rms and mean_rel of its own output against
 the FP32 golden on a seeded sample of output rows.
@@ -122,6 +127,37 @@ def time_per_step(fn, steps, warmup, flush=None):
             "total_ms": sum(samples)}
 
 
+def time_interleaved(fns, steps, warmup, rounds=5):
+    """Per-run timing of several paths in alternating rounds: every path gets exactly `steps`
+    calls, each under its own event pair as in time_per_step, split over `rounds` rounds whose
+    path order alternates (forward, then reversed), so that no path is timed only in a later,
+    hotter or more power-limited stretch of the run than another.  Median and mean (ms) per path."""
+    import torch
+    names = list(fns)
+    rounds = max(1, min(rounds, steps))
+    if rounds > 1:
+        for name in names:
+            warm(fns[name], warmup)
+    torch.cuda.synchronize()
+    samples = {name: [] for name in names}
+    for r in range(rounds):
+        n = steps // rounds + (1 if r < steps % rounds else 0)
+        for name in (names if r % 2 == 0 else names[::-1]):
+            fn = fns[name]
+            if rounds == 1:
+                warm(fn, warmup)   # path by path: each warmed right before its own calls
+            for _ in range(n):
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record()
+                fn()
+                end.record()
+                end.synchronize()
+                samples[name].append(start.elapsed_time(end))
+    torch.cuda.synchronize()
+    return {name: {"median_ms": statistics.median(v), "mean_ms": statistics.fmean(v), "total_ms": sum(v),
+                   "steps": len(v)} for name, v in samples.items()}
+
+
 def accuracy_of(case, prepared, inputs):
     """max_abs, rms and mean_rel of the path's output on a seeded sample of rows against the
     FP32 golden (performance/run.py:198-219 records the same per case)."""
@@ -138,20 +174,21 @@ def accuracy_of(case, prepared, inputs):
             "mean_rel": res["mean_rel"], "passed": res["passed"]}
 
 
-def measure_path(case, down, steps, warmup, inputs):
-    """Time whole steps, then the up and down kernels alone, for one down implementation."""
+def measure_path(case, down, steps, warmup, inputs, prepared=None):
+    """Whole steps back to back, then the up and down kernels alone, for one down implementation
+    (the per-run step time comes from time_interleaved)."""
     import ctypes
     import torch
     from ffn_optim_amd import _lib, prepare_ffn
     x, w1, w2 = inputs
-    prepared = prepare_ffn(x, w1, w2, down_impl=down)
+    if prepared is None:
+        prepared = prepare_ffn(x, w1, w2, down_impl=down)
     lib = _lib.load()
     plan = prepared.plan.native
     xs, w1s, w2s, hid, out, ws = prepared.tensors
     stream = torch.cuda.current_stream().cuda_stream
 
     torch.cuda.synchronize()
-    step = time_per_step(prepared.run, steps, warmup)
     step_b2b = time_back_to_back(prepared.run, steps, warmup)
 
     def up():
@@ -162,7 +199,7 @@ def measure_path(case, down, steps, warmup, inputs):
 
     t_up = time_back_to_back(up, steps, warmup)
     t_dn = time_back_to_back(dn, steps, warmup)
-    return prepared, step, step_b2b, t_up, t_dn
+    return prepared, step_b2b, t_up, t_dn
 
 
 def traffic_from_profiles(kernel_tag, case_id):
@@ -267,9 +304,10 @@ def cold_step_time(case, down, steps, inputs):
 
 
 def library_path(case, steps, warmup, inputs):
-    """torch's unfused eager path on the same inputs, timed like the fused path: GEMM
-    (hipBLASLt) -> F.gelu (exact) -> GEMM, with the hidden activation in the input dtype.  A
-    same-run yardstick for the fused operator; the golden stays the FP32 oracle."""
+    """torch's unfused eager path on the same inputs, as a callable timed like the fused path
+    (time_interleaved): GEMM (hipBLASLt) -> F.gelu (exact) -> GEMM, with the hidden activation in
+    the input dtype.  A same-run yardstick for the fused operator; the golden stays the FP32
+    oracle."""
     import torch
     import torch.nn.functional as F
     x, w1, w2 = inputs
@@ -279,8 +317,12 @@ def library_path(case, steps, warmup, inputs):
     def run():
         return F.gelu(x2 @ w1t) @ w2t
 
+    return run
+
+
+def library_record(case, step):
+    """The bench record of torch's unfused path from its per-run timing."""
     nums = workload_numbers(case)
-    step = time_per_step(run, steps, warmup)
     ms = step["median_ms"]
     return {"ms_per_step": ms, "tflops_4mkh": nums["flops_4mkh"] / ms / 1e9,
             "path": "torch eager: x @ w1.T (hipBLASLt), F.gelu, @ w2.T (hipBLASLt)"}
@@ -289,15 +331,26 @@ def library_path(case, steps, warmup, inputs):
 def bench_case(case, steps, warmup):
     import torch
     from ffn_optim_amd.cases import make_inputs
+    from ffn_optim_amd import prepare_ffn
     nums = workload_numbers(case)
     inputs = make_inputs(case, "cuda")
+    x, w1, w2 = inputs
     res = {}
+    preps = {}
     for down in ("basic", "streamk"):
         try:
-            prepared, step, step_b2b, t_up, t_dn = measure_path(case, down, steps, warmup, inputs)
+            preps[down] = prepare_ffn(x, w1, w2, down_impl=down)
         except ValueError as exc:
             res[down] = {"status": "not_applicable", "reason": str(exc)}
-            continue
+    # per-run step times of both fused paths and torch's unfused path, interleaved
+    fns = {down: p.run for down, p in preps.items()}
+    fns["torch_unfused"] = library_path(case, steps, warmup, inputs)
+    # A memory-bound workload's warm time depends on which weights the previous path left in the
+    # last-level cache: time it path by path (one round), and compare its cold times.
+    steps_of = time_interleaved(fns, steps, warmup, rounds=1 if case.get("memory_bound") else 5)
+    for down, prepared in list(preps.items()):
+        step = steps_of[down]
+        prepared, step_b2b, t_up, t_dn = measure_path(case, down, steps, warmup, inputs, prepared)
         ms = step["median_ms"]
         res[down] = {
             "ms_per_step": ms,
@@ -317,11 +370,12 @@ def bench_case(case, steps, warmup):
             "accuracy": accuracy_of(case, prepared, inputs),
         }
         del prepared
+        preps.pop(down)
         if case.get("memory_bound"):
             cold = cold_step_time(case, down, min(steps, 20), inputs)
             res[down].update(cold_ms_per_step=cold["median_ms"],
                              cold_hbm_gbs=nums["bytes"] / cold["median_ms"] / 1e6)
-    res["torch_unfused"] = library_path(case, steps, warmup, inputs)
+    res["torch_unfused"] = library_record(case, steps_of["torch_unfused"])
     torch.cuda.synchronize()
     return nums, res
 
