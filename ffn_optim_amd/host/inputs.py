@@ -84,7 +84,7 @@ def validate_tensors(x, weight1, weight2, layout="linear", require_device=False,
     """Tensor checks of ops/host/inputs.py:56-71; `require_device` asks for ROCm GPU tensors.
 
     require_npu is the reference's name of the same switch (ops/host/inputs.py:56), accepted
-    so that its callers run unchanged; it asks for the device this build runs on.  bias1
+    so that its callers run unchanged; it asks for the device the library runs on.  bias1
     ([H], or [2H] for SwiGLU) and bias2 ([N]) are given together or not at all, like the
     operands (same dtype and device, dense, no grad)."""
     import torch

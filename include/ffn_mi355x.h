@@ -241,7 +241,7 @@ int ffn_mi355x_variant_info(int variant, int* bm, int* bn, int* bk, int* waves, 
 
 /* Waves of a tile variant that only refill its LDS stages (0 for most tiles; `waves` above
  * counts them too), or a negative code for a variant out of range.  No counterpart in the
- * reference, whose tiles are fixed (ops/host/tiling.py:11-25): it describes this build's
+ * reference, whose tiles are fixed (ops/host/tiling.py:11-25): it describes the library's
  * tile table for planners and tests. */
 int ffn_mi355x_variant_refill_waves(int variant);
 

@@ -64,7 +64,9 @@ def run_prepared(x, w1, w2, **kw):
 @pytest.mark.parametrize("down", ["basic", "streamk"])
 @pytest.mark.parametrize("case_id", ["c1_smoke_fp16", "c2_aligned_bf16", "c3_unaligned_fp16",
                                      "c4_decode_bf16"])
-def test_baseline_case_full(case_id, down):
+def test_benchmark_case_full(case_id, down):
+    """Every benchmark workload but the DiT-size one (sampled rows, below), whole, on both down
+    paths, against the FP32 oracle with the reference's criterion."""
     case = get_case(case_id)
     say(case_id, down)
     x, w1, w2 = make_inputs(case, "cuda")

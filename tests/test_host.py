@@ -527,7 +527,7 @@ def test_streamk_grid_cuts_tiles_evenly_when_it_keeps_most_workgroups():
 
 def test_require_npu_is_the_reference_spelling_of_require_device():
     """Callers written against ops/host/inputs.py:56 pass require_npu; it means "the device
-    this build runs on" and rejects CPU tensors the same way."""
+    the library runs on" and rejects CPU tensors the same way."""
     import torch
     from ffn_optim_amd.host.inputs import validate_tensors
     x, a, b = torch.zeros(2, 3).half(), torch.zeros(4, 3).half(), torch.zeros(3, 4).half()
