@@ -61,6 +61,7 @@ CORE_SIGNATURES = {
     "ffn_mi355x_num_variants": (_i, []),
     "ffn_mi355x_variant_info": (_i, [_i, _P(_i), _P(_i), _P(_i), _P(_i), _P(_i), _P(_i)]),
     "ffn_mi355x_variant_refill_waves": (_i, [_i]),
+    "ffn_mi355x_variant_mfma_edge": (_i, [_i]),
     "ffn_mi355x_last_error": (ctypes.c_char_p, []),
     "ffn_mi355x_strerror": (ctypes.c_char_p, [_i]),
     "ffn_mi355x_version": (ctypes.c_char_p, []),
@@ -216,6 +217,8 @@ def variants() -> list[dict]:
         check(lib.ffn_mi355x_variant_info(v, *map(ctypes.byref, vals)))
         refill = lib.ffn_mi355x_variant_refill_waves(v)
         check(min(refill, 0))
+        edge = lib.ffn_mi355x_variant_mfma_edge(v)
+        check(min(edge, 0))
         out.append(dict(zip(("bm", "bn", "bk", "waves", "stages", "lds_bytes"),
-                            (x.value for x in vals)), variant=v, refill_waves=refill))
+                            (x.value for x in vals)), variant=v, refill_waves=refill, mfma_edge=edge))
     return out

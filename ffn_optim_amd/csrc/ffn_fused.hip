@@ -58,7 +58,7 @@ struct TileBody {
     __device__ __forceinline__ void run() {
         static_assert(C::PROD == 0 || epi_in_regs<C, EPI, false>() || C::WGK > 1, "refill waves: no staged epilogue");
         Engine<DT, C, false, ISSUE, MMA> eng(smem, p);
-        f32x16 acc[C::FN][C::FM];
+        typename AccOf<C::MF>::type acc[C::FN][C::FM];
         Unit none = u;
         none.valid = false;
         eng.prologue(p, u);

@@ -10,16 +10,20 @@
 //
 // Data path of one macro tile (BM x BN, reduction step BK):
 //   HBM/L2 --buffer_load_dwordx4 ... lds--> LDS stage s  (no VGPR staging)
-//   LDS --ds_read_b128--> A/B fragments --v_mfma_f32_32x32x16_{bf16,f16}--> FP32 acc
+//   LDS --ds_read_b128--> A/B fragments --v_mfma_f32_32x32x16 or 16x16x32_{bf16,f16}--> FP32 acc
 // LDS rows are BK*2 bytes; the 16-byte chunk c of row r lives at c ^ ((r / R256) mod CH),
 // R256 = rows per 256-byte line of the 64 LDS banks: the 16 lanes of one ds_read_b128 cycle
-// (16 consecutive rows, one chunk) then cover all 64 banks exactly once.  Out-of-range
+// (16 consecutive rows, one chunk) then cover all 64 banks exactly once.  That holds for both
+// fragment shapes: a 32x32x16 fragment gives lanes 0-31 rows 0-31 and lanes 32-63 the next
+// chunk of the same rows, a 16x16x32 fragment gives each 16 lanes rows 0-15 and one of four
+// consecutive chunks.  Out-of-range
 // rows and the K tail read as zero through the buffer descriptor's range check,
 // so tiles may overhang the matrices and no load can leave its buffer.
 //
 // The MFMA is issued with the weight fragment as operand A and the activation
 // fragment as operand B, so an accumulator holds D[n][m]; each lane then owns
-// four consecutive n of one row m and the epilogue writes 8-byte packed stores.
+// groups of four consecutive n of one row m, which the epilogue packs into 8 bytes and pairs
+// across lanes into 16-byte stores.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -108,7 +112,7 @@ struct FusedParams {
 // WTM x WTN wave tile over its own BK/WGK slice of every stage, and the WGK partial tiles are
 // summed through LDS after the main loop.
 template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int STAGES_, int SYNCQ_ = -1, int DMAKS_ = -1,
-          int WGK_ = 1, int DMAW_ = 0, int PROD_ = 0, int EARLY_ = 0>
+          int WGK_ = 1, int DMAW_ = 0, int PROD_ = 0, int EARLY_ = 0, int MF_ = 32>
 struct TileCfg {
     static constexpr int BM = BM_, BN = BN_, BK = BK_;
     static constexpr int WGM = WGM_, WGN = WGN_, WGK = WGK_, STAGES = STAGES_;
@@ -119,7 +123,15 @@ struct TileCfg {
     static constexpr int PROD = PROD_;
     static constexpr int NT = (NW + PROD) * 64;    // threads per workgroup
     static constexpr int WTM = BM / WGM, WTN = BN / WGN;  // wave tile
-    static constexpr int FM = WTM / 32, FN = WTN / 32;    // 32x32 MFMA blocks per wave
+    // MFMA block edge: 32 (v_mfma_f32_32x32x16, 16 accumulators per lane) or 16
+    // (v_mfma_f32_16x16x32, 4 per lane).  Same FLOPs per LDS byte for a given wave tile; the
+    // 16x16x32 form takes less energy per FLOP, which counts where the clock is held down by
+    // the activity of the whole chip.
+    static constexpr int MF = MF_;
+    static_assert(MF_ == 32 || MF_ == 16, "MFMA blocks are 32x32x16 or 16x16x32");
+    static constexpr int KSTEP_K = 512 / MF;       // reduction depth of one MFMA
+    static constexpr int FM = WTM / MF, FN = WTN / MF;    // MFMA blocks per wave
+    static_assert(MF == 32 || (FM % 2 == 0 && FN % 2 == 0), "16x16 blocks go in pairs");
     static constexpr int ROWB = BK * 2;            // bytes of one LDS row
     static constexpr int CH = ROWB / 16;           // 16-byte chunks per row
     static constexpr int RPB = 1024 / ROWB;        // rows per 1 KiB DMA block (64 lanes x 16 B)
@@ -146,7 +158,7 @@ struct TileCfg {
     static_assert(EARLY_ == 0 || (STAGES_ == 2 && WGK_ == 1 && EARLY_ < A_PW + B_PW),
                   "early refill: two stages, no K slices, part of the refill");
     static constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
-    static constexpr int KSTEPS = BK / 16 / WGK;   // MFMA k-steps per stage and wave
+    static constexpr int KSTEPS = BK / KSTEP_K / WGK;  // MFMA k-steps per stage and wave
     // Output staging of the epilogue: from stage STAGES-1 (which the next unit's DMA prologue
     // leaves free) up to EPI_AVAIL bytes.  A workgroup whose stages take more than half of the
     // LDS runs alone on its CU, so it may use all 160 KiB; a smaller one keeps to one stage and
@@ -172,10 +184,11 @@ struct TileCfg {
     static_assert(ER > 0, "no output chunk of whole 32-row blocks fits the staging area");
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
     static_assert(ROWB % 16 == 0 && CH >= 2, "BK must be a multiple of 16");
-    static_assert(BK % (16 * WGK) == 0, "every wave takes whole k-steps of a stage");
+    static_assert(BK % (KSTEP_K * WGK) == 0, "every wave takes whole k-steps of a stage");
+    static_assert(MF == 32 || WGK == 1, "16x16x32 blocks: no K slices (their exchange moves 32x32 blocks)");
     static_assert(NW % DW == 0 && A_BLKS % DW == 0 && B_BLKS % DW == 0,
                   "DMA blocks must split evenly over the issuing waves");
-    static_assert(32 % (CH * R256) == 0, "fragment rows start on a swizzle period");
+    static_assert(MF % (CH * R256) == 0, "fragment rows start on a swizzle period");
     // DMA offset sets a lane keeps: one per block of the swizzle period (at least two)
     static constexpr int NPAR = SWZ_PERIOD > 2 ? SWZ_PERIOD : 2;
     static_assert(SWZ_PERIOD <= 4, "at most four DMA offset sets");
@@ -231,6 +244,24 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                       __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
+template <int DT>
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+    if constexpr (DT == DT_BF16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+// accumulator of one MFMA block: 16 FP32 per lane for 32x32, 4 for 16x16
+template <int MF>
+struct AccOf {
+    using type = f32x16;
+};
+template <>
+struct AccOf<16> {
+    using type = f32x4;
+};
 
 // Bit reinterpretation of one 32-bit value, taken by value: __builtin_bit_cast applied
 // directly to an element of an ext_vector_type (v.y, acc[k]) reads element 0 of the vector
@@ -445,6 +476,11 @@ template <int DT, class C, bool GA, bool ISSUE, bool MMA>
 struct Engine {
     static constexpr int FM = C::FM, FN = C::FN, NT = C::NT, S = C::STAGES, KS = C::KSTEPS;
     static_assert(KS % 2 == 0, "fragment double-buffer assumes an even number of k-steps per wave");
+    static constexpr int MF = C::MF;
+    using Acc = typename AccOf<MF>::type;
+    static constexpr int NQ = MF == 32 ? 4 : 1;  // groups of four accumulators per block
+    static constexpr int CPK = C::KSTEP_K / 8;   // 16-byte K chunks of one k-step (2 or 4)
+    static constexpr int LSH = MF == 32 ? 5 : 4; // lane >> LSH: this lane's chunk of the k-step
 
     lds_char* smem;
     int tid, lane, wave, wm, wn, wk;
@@ -462,11 +498,11 @@ struct Engine {
         wm = tw % C::WGM;
         wn = C::WGK == 1 ? tw / C::WGM : (tw / C::WGM) % C::WGN;
         wk = C::WGK == 1 ? 0 : tw / (C::WGM * C::WGN);
-        const int r = lane & 31;
+        const int r = lane & (MF - 1);
         a_row_off = (wm * C::WTM + r) * C::ROWB;
         b_row_off = C::A_BYTES + (wn * C::WTN + r) * C::ROWB;
         swz = swz_of(r);
-        khalf = 2 * KS * wk + (lane >> 5);
+        khalf = CPK * KS * wk + (lane >> LSH);
     }
 
     __device__ __forceinline__ void rsrc(const GemmParams& p, const Unit& u,
@@ -633,25 +669,32 @@ struct Engine {
 
     // Fragment registers: A (activation rows) double-buffered across k-steps, B (weight rows)
     // reloaded in place right after its last use, which the j-major MFMA order makes early.
-    u32x4 fa[2][FM], fb[FN];
+    // SPLIT (16x16x32 blocks): the MFMAs of a k-step go in two halves, each over half of the A
+    // fragments (j-major inside a half), so every A and B fragment has its last use well before
+    // the end of the k-step and is read again into the same registers right after it.  One
+    // buffer of each instead of two for A: the 16-row fragments of a 64x128 wave tile would
+    // otherwise hold 64 VGPRs beside the 128 accumulators.
+    static constexpr bool SPLIT = MF == 16;
+    static_assert(!SPLIT || FM % 2 == 0, "the split order halves the A fragments");
+    u32x4 fa[SPLIT ? 1 : 2][FM], fb[FN];
 
     // byte offset in its row of this lane's 16-byte K chunk for k-step ks of the wave's slice
-    int khalf;  // 2 * (first k-step of the wave's slice) + (lane >> 5)
+    int khalf;  // CPK * (first k-step of the wave's slice) + (lane >> LSH)
     __device__ __forceinline__ int frag_chunk(int ks) const {
-        return ((2 * ks + khalf) ^ swz) * 16;
+        return ((CPK * ks + khalf) ^ swz) * 16;
     }
     template <int BUF, int I>
     __device__ __forceinline__ void read_a(int stage, int ks) {
         if constexpr (MMA) {
             const lds_char* st = smem + stage * C::STAGE_BYTES;
-            fa[BUF][I] = *(const __attribute__((address_space(3))) u32x4*)(st + a_row_off + I * 32 * C::ROWB + frag_chunk(ks));
+            fa[BUF][I] = *(const __attribute__((address_space(3))) u32x4*)(st + a_row_off + I * MF * C::ROWB + frag_chunk(ks));
         }
     }
     template <int J>
     __device__ __forceinline__ void read_b(int stage, int ks) {
         if constexpr (MMA) {
             const lds_char* st = smem + stage * C::STAGE_BYTES;
-            fb[J] = *(const __attribute__((address_space(3))) u32x4*)(st + b_row_off + J * 32 * C::ROWB + frag_chunk(ks));
+            fb[J] = *(const __attribute__((address_space(3))) u32x4*)(st + b_row_off + J * MF * C::ROWB + frag_chunk(ks));
         }
     }
     template <int BUF, int I0, int I1>
@@ -684,15 +727,42 @@ struct Engine {
     static constexpr int NM = FN * FM;
     // slot of the last k-step after whose MFMA the stage wait + barrier is placed: the end of
     // the j = 0 block, from where every B fragment can be reloaded after its last use
-    static constexpr int SYNC_Q = C::SYNCQ >= 0 ? C::SYNCQ : FM - 1;
+    static constexpr int SYNC_Q = C::SYNCQ >= 0 ? C::SYNCQ : SPLIT ? NM / 2 - 1 : FM - 1;
     static_assert(SYNC_Q >= FM - 1 && SYNC_Q < NM, "the barrier may not precede the in-place B reloads");
-    // Slots carrying the refill DMA.  With two stages the data is waited for at the end of the
-    // same iteration, so it goes out in the first DMAKS k-steps (default: the first half).  With
-    // more, it is spread over every
-    // slot before the stage wait, or (DMAKS == KS) over every slot of the iteration: the
-    // stage wait then also allows the part of this iteration's group issued after it.
-    static constexpr bool DMA_ALL = S > 2 && C::DMAKS == KS;
-    static constexpr int DMA_SLOTS = (S == 2)  ? (C::DMAKS > 0 ? C::DMAKS : KS / 2) * NM
+    // slot of a unit's last k-step after which the barrier and the next unit's DMA prologue go.
+    // The split order reads no fragment in that k-step, so they wait for its last MFMA, when no
+    // fragment register is live beside the accumulators and the prologue's addressing.
+    static constexpr int PRO_Q = SPLIT ? NM - 1 : SYNC_Q;
+    // Split order: slot Q of a k-step takes block (slot_j(Q), slot_i(Q)); last_a(i) / last_b(j)
+    // is the last slot using A fragment i / B fragment j.
+    static constexpr int HS = NM / 2, FMH = FM / 2;
+    static constexpr int slot_i(int Q) { return (Q / HS) * FMH + (Q % HS) % FMH; }
+    static constexpr int slot_j(int Q) { return (Q % HS) / FMH; }
+    static constexpr int last_a(int i) { return (i / FMH) * HS + (FN - 1) * FMH + i % FMH; }
+    static constexpr int last_b(int j) { return HS + j * FMH + FMH - 1; }
+    // Split order: the fragment reads of slot Q -- fragment X (A for X < FM, B after) is read at
+    // max(its last use, FLOOR) -- from `stage`, k-step ks.
+    template <int Q, int FLOOR, int X>
+    __device__ __forceinline__ void reread_at(int stage, int ks) {
+        if constexpr (X < FM + FN) {
+            if constexpr (X < FM) {
+                if constexpr ((last_a(X) > FLOOR ? last_a(X) : FLOOR) == Q) read_a<0, X>(stage, ks);
+            } else {
+                if constexpr ((last_b(X - FM) > FLOOR ? last_b(X - FM) : FLOOR) == Q) read_b<X - FM>(stage, ks);
+            }
+            reread_at<Q, FLOOR, X + 1>(stage, ks);
+        }
+    }
+    // Slots carrying the refill DMA.  DMAKS counts 16-deep steps of K: k-steps of 32x32x16 blocks,
+    // halves of 16x16x32 ones.  With two stages the data is waited for at the end of the same
+    // iteration, so it goes out in the slots of the first DMAKS * 16 K elements of the iteration
+    // (default: the first half).  With more, it is spread over every slot before the stage
+    // wait, or (DMAKS covering the whole stage) over every slot of the iteration: the stage
+    // wait then also allows the part of this iteration's group issued after it.
+    static constexpr bool DMA_ALL = S > 2 && C::DMAKS * 16 == KS * C::KSTEP_K;
+    static_assert(S != 2 || C::DMAKS <= 0 || (C::DMAKS * NM * 16) % C::KSTEP_K == 0,
+                  "the refill window covers whole slots");
+    static constexpr int DMA_SLOTS = (S == 2)  ? (C::DMAKS > 0 ? C::DMAKS * NM * 16 / C::KSTEP_K : KS / 2 * NM)
                                      : DMA_ALL ? KS * NM
                                                : (KS - 1) * NM + SYNC_Q;
     static_assert(DMA_SLOTS >= 1, "at least one slot carries the refill");
@@ -719,13 +789,19 @@ struct Engine {
     }
 
     template <bool FAST, int CB, int MODE, bool DMA, int KSI, int Q>
-    __device__ __forceinline__ void slot(const GemmParams& p, f32x16 (&acc)[FN][FM], int cur, int nxt,
+    __device__ __forceinline__ void slot(const GemmParams& p, Acc (&acc)[FN][FM], int cur, int nxt,
                                          const __amdgpu_buffer_rsrc_t& ra, const __amdgpu_buffer_rsrc_t& rb,
                                          int dma_stage, const DmaLane& L, const DmaIt& o, const Unit& nx) {
-        constexpr int j = Q / FM, i = Q % FM;
-        if constexpr (MMA) acc[j][i] = mfma32<DT>(fb[j], fa[CB][i], acc[j][i]);
+        constexpr int j = SPLIT ? slot_j(Q) : Q / FM, i = SPLIT ? slot_i(Q) : Q % FM;
+        if constexpr (MMA) {
+            if constexpr (MF == 32) acc[j][i] = mfma32<DT>(fb[j], fa[CB][i], acc[j][i]);
+            else acc[j][i] = mfma16<DT>(fb[j], fa[0][i], acc[j][i]);
+        }
         constexpr int NB = 1 - CB;
-        if constexpr (MODE == 0) {
+        if constexpr (MODE == 0 && SPLIT) {
+            // the fragments whose last use in this k-step was this slot, for the next k-step
+            reread_at<Q, -1, 0>(cur, KSI + 1);
+        } else if constexpr (MODE == 0) {
             // A fragments of the next k-step over the first half of the slots; B fragment j
             // right after its last use (the end of block j)
             constexpr int half = NM / 2 > 0 ? NM / 2 : 1;
@@ -733,24 +809,29 @@ struct Engine {
             if constexpr (Q < half) read_a_range<NB, a0, (a1 < FM ? a1 : FM)>(cur, KSI + 1);
             if constexpr (i == FM - 1) read_b<j>(cur, KSI + 1);
         } else {
-            if constexpr (Q == SYNC_Q) {
-                if constexpr (MODE == 1) {
-                    // every wave's DMA of the next stage has landed; every wave is done with the
-                    // stage the next refill overwrites
-                    wait_vmcnt<(S == 2 ? 0 : STAGE_WAIT)>();
-                    barrier();
-                } else if (nx.valid) {
+            if constexpr (MODE == 1 && Q == SYNC_Q) {
+                // every wave's DMA of the next stage has landed; every wave is done with the
+                // stage the next refill overwrites
+                wait_vmcnt<(S == 2 ? 0 : STAGE_WAIT)>();
+                barrier();
+            } else if constexpr (MODE == 2 && Q == PRO_Q) {
+                if (nx.valid) {
                     barrier();
                     prologue(p, nx);
                 }
             }
             if constexpr (MODE == 1 && Q >= SYNC_Q) {
                 constexpr int span = NM - SYNC_Q, qq = Q - SYNC_Q;
-                constexpr int a0 = qq * FM / span, a1 = (qq + 1) * FM / span;
-                read_a_range<NB, a0, a1>(nxt, 0);
-                // B fragment jj is reloaded once both its last use (the end of block jj) and
-                // the barrier are behind
-                reload_b_at<Q, 0>(nxt);
+                if constexpr (SPLIT) {
+                    // each fragment once both its last use and the barrier are behind
+                    reread_at<Q, SYNC_Q, 0>(nxt, 0);
+                } else {
+                    constexpr int a0 = qq * FM / span, a1 = (qq + 1) * FM / span;
+                    read_a_range<NB, a0, a1>(nxt, 0);
+                    // B fragment jj is reloaded once both its last use (the end of block jj)
+                    // and the barrier are behind
+                    reload_b_at<Q, 0>(nxt);
+                }
                 // the stage this iteration read is free: the early part of the iteration after
                 // next goes into it (range-checked: that iteration may be a K tail or past the
                 // unit, which reads zeros)
@@ -770,7 +851,7 @@ struct Engine {
     }
 
     template <bool FAST, int CB, int MODE, bool DMA, int KSI, int Q>
-    __device__ __forceinline__ void slots(const GemmParams& p, f32x16 (&acc)[FN][FM], int cur, int nxt,
+    __device__ __forceinline__ void slots(const GemmParams& p, Acc (&acc)[FN][FM], int cur, int nxt,
                                           const __amdgpu_buffer_rsrc_t& ra, const __amdgpu_buffer_rsrc_t& rb,
                                           int dma_stage, const DmaLane& L, const DmaIt& o, const Unit& nx) {
         if constexpr (Q < NM) {
@@ -783,7 +864,7 @@ struct Engine {
     __device__ __forceinline__ void ksteps(const GemmParams& p, const Unit& nx,
                                            const __amdgpu_buffer_rsrc_t& ra,
                                            const __amdgpu_buffer_rsrc_t& rb, int cur, int dstage,
-                                           const DmaLane& L, const DmaIt& o, f32x16 (&acc)[FN][FM]) {
+                                           const DmaLane& L, const DmaIt& o, Acc (&acc)[FN][FM]) {
         if constexpr (KSI < KS) {
             constexpr int MODE = (KSI + 1 < KS) ? 0 : (LAST ? 2 : 1);
             const int nxt = (cur + 1 == S) ? 0 : cur + 1;
@@ -799,7 +880,7 @@ struct Engine {
     template <bool FAST>
     __device__ __forceinline__ void step(const GemmParams& p, const Unit& u, const Unit& nx,
                                          const __amdgpu_buffer_rsrc_t& ra, const __amdgpu_buffer_rsrc_t& rb,
-                                         const DmaLane& L, f32x16 (&acc)[FN][FM], int& cur, int it, int n) {
+                                         const DmaLane& L, Acc (&acc)[FN][FM], int& cur, int it, int n) {
         const int dkit = it + S - 1;
         DmaIt o = dma_it(p, u.kb + dkit, FAST || dkit < n);
         if constexpr (C::EARLY > 0) {
@@ -823,12 +904,12 @@ struct Engine {
     // order against, so that unit waits for everything.)
     template <bool FASTK>
     __device__ __forceinline__ void mainloop(const GemmParams& p, const Unit& u, const Unit& nx,
-                                             f32x16 (&acc)[FN][FM], bool first = false) {
+                                             Acc (&acc)[FN][FM], bool first = false) {
         if constexpr (MMA) {
 #pragma unroll
             for (int j = 0; j < FN; ++j)
 #pragma unroll
-                for (int i = 0; i < FM; ++i) acc[j][i] = f32x16{};
+                for (int i = 0; i < FM; ++i) acc[j][i] = Acc{};
         }
         __amdgpu_buffer_rsrc_t ra, rb;
         rsrc(p, u, ra, rb);
@@ -880,7 +961,7 @@ struct Engine {
     // 2q, 2q+1 of acc[j][i], whose sources are already consumed.
     template <int EPI, bool BIAS>
     __device__ __forceinline__ void activate_chunk(const GemmParams& p, const Unit& u, int c,
-                                                   f32x16 (&acc)[FN][FM]) const {
+                                                   Acc (&acc)[FN][FM]) const {
         const int bcol = u.tn * C::BN + wn * C::WTN + 4 * (lane >> 5);
 #pragma unroll
         for (int ib = 0; ib < BPC; ++ib) {
@@ -900,16 +981,17 @@ struct Engine {
 
     template <int EPI>
     __device__ __forceinline__ void store_tile_lds(const GemmParams& p, const Unit& u, bool next,
-                                                   f32x16 (&acc)[FN][FM]) {
+                                                   Acc (&acc)[FN][FM]) {
         if (p.bias) store_tile_lds_as<EPI, true>(p, u, next, acc);
         else store_tile_lds_as<EPI, false>(p, u, next, acc);
     }
     template <int EPI, bool BIAS>
     __device__ __forceinline__ void store_tile_lds_as(const GemmParams& p, const Unit& u, bool next,
-                                                      f32x16 (&acc)[FN][FM]) {
+                                                      Acc (&acc)[FN][FM]) {
         static_assert(C::OUT_POW2, "the staging swizzle needs a power-of-two number of pieces per row");
         static_assert((ER * TPR) % NT == 0, "chunk pieces split evenly over the threads");
         static_assert(C::EARLY == 0, "the next unit's early refill fills part of the staging stage");
+        static_assert(C::MF == 32, "the staged epilogue moves 32x32 blocks");
         lds_char* eb = smem + C::EPI_OFF;
         // DMA still in flight may target any stage but the next unit's prologue (issued last):
         // drain it; the barrier before the first staging write makes sure every wave has
@@ -983,7 +1065,7 @@ struct Engine {
     // Bias (if any) added to acc's columns: group q of block j holds columns
     // col0 + 32j + 8q + 4h + 0..3 of the tile, h = lane >> 5.
     template <int EPI, bool BIAS>
-    __device__ __forceinline__ u32x2 out4(const GemmParams& p, const f32x16& a, int q, int col) const {
+    __device__ __forceinline__ u32x2 out4(const GemmParams& p, const Acc& a, int q, int col) const {
         if constexpr (BIAS) {
             const f32x4 b = bias4<DT>(p, col);
             return pack4<DT>(activate<EPI>(a[4 * q] + b.x), activate<EPI>(a[4 * q + 1] + b.y),
@@ -995,7 +1077,7 @@ struct Engine {
     }
     // SwiGLU: SiLU(gate + its bias) * (up + its bias) of the matching groups of a block pair.
     template <bool BIAS>
-    __device__ __forceinline__ u32x2 swiglu4(const GemmParams& p, const f32x16& g, const f32x16& up, int q,
+    __device__ __forceinline__ u32x2 swiglu4(const GemmParams& p, const Acc& g, const Acc& up, int q,
                                              int gcol, int ucol) const {
         f32x4 bg = {0.0f, 0.0f, 0.0f, 0.0f}, bu = bg;
         if constexpr (BIAS) bg = bias4<DT>(p, gcol), bu = bias4<DT>(p, ucol);
@@ -1017,13 +1099,68 @@ struct Engine {
     }
     template <int EPI, int I0 = 0, int I1 = FM>
     __device__ __forceinline__ void store_tile_regs(const GemmParams& p, const Unit& u,
-                                                    f32x16 (&acc)[FN][FM]) const {
-        if (p.bias) store_tile_regs_as<EPI, I0, I1, true>(p, u, acc);
-        else store_tile_regs_as<EPI, I0, I1, false>(p, u, acc);
+                                                    Acc (&acc)[FN][FM]) const {
+        static_assert(0 <= I0 && I0 <= I1 && I1 <= FM, "accumulator block rows");
+        if constexpr (MF == 16) {
+            if (p.bias) store_tile_regs16_as<EPI, I0, I1, true>(p, u, acc);
+            else store_tile_regs16_as<EPI, I0, I1, false>(p, u, acc);
+        } else {
+            if (p.bias) store_tile_regs_as<EPI, I0, I1, true>(p, u, acc);
+            else store_tile_regs_as<EPI, I0, I1, false>(p, u, acc);
+        }
+    }
+    // 16x16 blocks: lane l holds columns 4g..4g+3 (g = l >> 4) of row l & 15 of every block.
+    // For two blocks X and Y of a row, one v_permlane16_swap per word (lanes of 16-lane row 2r+1
+    // of X trade with those of row 2r of Y) leaves each lane 8 consecutive columns of one block:
+    // lanes of rows 0 and 2 columns 0-7 and 8-15 of X, rows 1 and 3 the same of Y.  n is the
+    // lane's first output column after the swap.
+    __device__ __forceinline__ void store_pair16(const GemmParams& p, char* row, int m, int n, u32x2 x, u32x2 y) const {
+        const auto s0 = __builtin_amdgcn_permlane16_swap(x.x, y.x, false, false);
+        const auto s1 = __builtin_amdgcn_permlane16_swap(x.y, y.y, false, false);
+        const u32x4 v = {(uint32_t)s0[0], (uint32_t)s1[0], (uint32_t)s0[1], (uint32_t)s1[1]};
+        if (m < p.M && n < p.c_cols) *(u32x4*)(row + (size_t)n * 2) = v;
+    }
+    // Block rows [I0, I1) of the wave tile, 16x16 blocks.
+    template <int EPI, int I0, int I1, bool BIAS>
+    __device__ __forceinline__ void store_tile_regs16_as(const GemmParams& p, const Unit& u,
+                                                         Acc (&acc)[FN][FM]) const {
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int g = ln >> 4;
+        const int m0 = u.tm * C::BM + wm * C::WTM + (ln & 15);
+        const int col0 = u.tn * C::BN + wn * C::WTN;   // first column of the wave tile
+        const int bcol = col0 + 4 * g;                  // the lane's bias columns in block 0
+        const int scol = 16 * (g & 1) + 8 * (g >> 1);   // its 8 columns of a block pair after the swap
+#pragma unroll
+        for (int i = I0; i < I1; ++i) {
+            const int m = m0 + 16 * i;
+            char* row = (char*)p.c + (size_t)m * (size_t)p.ldc * 2;
+            if constexpr (EPI == EPI_SWIGLU) {
+                // gate columns 64k + 0..31 are blocks 4k, 4k+1, their up columns blocks 4k+2, 4k+3
+                static_assert(FN % 4 == 0, "SwiGLU pairs the 32-column groups of a wave tile");
+#pragma unroll
+                for (int k = 0; k < FN / 4; ++k) {
+                    const u32x2 x = swiglu4<BIAS>(p, acc[4 * k][i], acc[4 * k + 2][i], 0, bcol + 64 * k,
+                                                  bcol + 64 * k + 32);
+                    const u32x2 y = swiglu4<BIAS>(p, acc[4 * k + 1][i], acc[4 * k + 3][i], 0, bcol + 64 * k + 16,
+                                                  bcol + 64 * k + 48);
+                    store_pair16(p, row, m, col0 / 2 + 32 * k + scol, x, y);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < FN / 2; ++k) {
+                    const u32x2 x = out4<EPI, BIAS>(p, acc[2 * k][i], 0, bcol + 32 * k);
+                    const u32x2 y = out4<EPI, BIAS>(p, acc[2 * k + 1][i], 0, bcol + 32 * k + 16);
+                    store_pair16(p, row, m, col0 + 32 * k + scol, x, y);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        }
     }
     template <int EPI, int I0, int I1, bool BIAS>
     __device__ __forceinline__ void store_tile_regs_as(const GemmParams& p, const Unit& u,
-                                                       f32x16 (&acc)[FN][FM]) const {
+                                                       Acc (&acc)[FN][FM]) const {
         int ln = lane;
         asm volatile("" : "+v"(ln));
         const int m0 = u.tm * C::BM + wm * C::WTM + (ln & 31);
@@ -1080,7 +1217,7 @@ struct Engine {
     // Block b (0-based) of the ROWS x FN blocks owned by a slice whose rows start at BASE: row
     // block BASE + b % ROWS, column block b / ROWS.
     template <int ROWS, int BASE, int B0, int B1>
-    __device__ __forceinline__ void xsend(lds_char* area, f32x16 (&acc)[FN][FM]) const {
+    __device__ __forceinline__ void xsend(lds_char* area, Acc (&acc)[FN][FM]) const {
         if constexpr (B0 < B1) {
             constexpr int j = B0 / ROWS, i = BASE + B0 % ROWS, sl = B0 % XB;
 #pragma unroll
@@ -1091,7 +1228,7 @@ struct Engine {
         }
     }
     template <int ROWS, int BASE, int B0, int B1>
-    __device__ __forceinline__ void xrecv(const lds_char* area, f32x16 (&acc)[FN][FM]) const {
+    __device__ __forceinline__ void xrecv(const lds_char* area, Acc (&acc)[FN][FM]) const {
         if constexpr (B0 < B1) {
             constexpr int j = B0 / ROWS, i = BASE + B0 % ROWS, sl = B0 % XB;
 #pragma unroll
@@ -1105,7 +1242,7 @@ struct Engine {
     }
     static constexpr int clampb(int v, int hi) { return v < hi ? v : hi; }
     template <int WK, int PH>
-    __device__ __forceinline__ void xphases(f32x16 (&acc)[FN][FM]) const {
+    __device__ __forceinline__ void xphases(Acc (&acc)[FN][FM]) const {
         if constexpr (PH * XB < XMAX) {
             // this slice sends the partner's blocks and receives its own; both lists run in
             // phases of XB blocks (every wave passes the same barriers, also with nothing to send)
@@ -1124,7 +1261,7 @@ struct Engine {
     }
     template <int EPI, int WK>
     __device__ __forceinline__ void store_sliced_as(const GemmParams& p, const Unit& u, bool next,
-                                                    f32x16 (&acc)[FN][FM]) {
+                                                    Acc (&acc)[FN][FM]) {
         // DMA still in flight may target any stage but the next unit's prologue (issued last):
         // drain it; the barrier makes sure every wave has before the area is written
         if (next) wait_vmcnt<PRO_LOADS>();
@@ -1151,14 +1288,14 @@ struct Engine {
     }
     template <int EPI>
     __device__ __forceinline__ void store_sliced(const GemmParams& p, const Unit& u, bool next,
-                                                 f32x16 (&acc)[FN][FM]) {
+                                                 Acc (&acc)[FN][FM]) {
         // one static body per slice (acc is dead after either)
         if (wk == 0) store_sliced_as<EPI, 0>(p, u, next, acc);
         else store_sliced_as<EPI, 1>(p, u, next, acc);
     }
 
     // FP32 partial tile in the accumulator's own register order: group (j, i, q) of logical
-    // thread t lives at ((j*FM + i)*4 + q)*NTL + t (16-byte units), so every store is coalesced.
+    // thread t lives at ((j*FM + i)*NQ + q)*NTL + t (16-byte units), so every store is coalesced.
     // t is the thread's index among the WGM x WGN tile waves of one K slice, NTL their thread
     // count: a K-sliced tile first sums its slices (the exchange above) and each slice then
     // writes the row blocks [I0, I1) it owns.  (Refill-only waves, numbered first, hold none.)
@@ -1167,19 +1304,20 @@ struct Engine {
     static __device__ __forceinline__ uint32_t part_off(int idx, int t) { return (uint32_t)(idx * NTL + t) * 16u; }
     template <int I0 = 0, int I1 = FM>
     __device__ __forceinline__ void store_partial(const __amdgpu_buffer_rsrc_t& r, uint32_t slot_off,
-                                                  f32x16 (&acc)[FN][FM]) const {
+                                                  Acc (&acc)[FN][FM]) const {
+        static_assert(0 <= I0 && I0 <= I1 && I1 <= FM, "accumulator block rows");
         const int t = slice_thread();
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int i = I0; i < I1; ++i)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int idx = (j * FM + i) * 4 + q;
+                for (int q = 0; q < NQ; ++q) {
+                    const int idx = (j * FM + i) * NQ + q;
                     const f32x4 v = {acc[j][i][4 * q], acc[j][i][4 * q + 1], acc[j][i][4 * q + 2],
                                      acc[j][i][4 * q + 3]};
                     store_coherent(r, slot_off + part_off(idx, t), v);
-                    if (q == 3) __builtin_amdgcn_sched_barrier(0);
+                    if (q == NQ - 1) __builtin_amdgcn_sched_barrier(0);
                 }
     }
 
@@ -1189,22 +1327,23 @@ struct Engine {
     // one piece after another.
     template <int PC, int I0, int I1>
     __device__ __forceinline__ void add_pieces(const __amdgpu_buffer_rsrc_t& r, const uint32_t (&so)[PC], int c,
-                                               bool set, int t, f32x16 (&acc)[FN][FM]) const {
+                                               bool set, int t, Acc (&acc)[FN][FM]) const {
+        static_assert(0 <= I0 && I0 <= I1 && I1 <= FM, "accumulator block rows");
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int i = I0; i < I1; ++i) {
-                f32x4 g[PC][4];
+                f32x4 g[PC][NQ];
 #pragma unroll
                 for (int k = 0; k < PC; ++k)
                     if (k < c)
 #pragma unroll
-                        for (int q = 0; q < 4; ++q) g[k][q] = load_coherent(r, so[k] + part_off((j * FM + i) * 4 + q, t));
+                        for (int q = 0; q < NQ; ++q) g[k][q] = load_coherent(r, so[k] + part_off((j * FM + i) * NQ + q, t));
 #pragma unroll
                 for (int k = 0; k < PC; ++k)
                     if (k < c)
 #pragma unroll
-                        for (int q = 0; q < 4; ++q)
+                        for (int q = 0; q < NQ; ++q)
 #pragma unroll
                             for (int e = 0; e < 4; ++e)
                                 acc[j][i][4 * q + e] = (set && k == 0) ? g[k][q][e] : acc[j][i][4 * q + e] + g[k][q][e];
@@ -1223,7 +1362,8 @@ struct Engine {
     // every piece is read back.
     template <int EPI, int I0, int I1>
     __device__ __forceinline__ void finish_piece(const GemmParams& p, const Unit& u, int v,
-                                                 const __amdgpu_buffer_rsrc_t& r, f32x16 (&acc)[FN][FM]) {
+                                                 const __amdgpu_buffer_rsrc_t& r, Acc (&acc)[FN][FM]) {
+        static_assert(0 <= I0 && I0 <= I1 && I1 <= FM, "accumulator block rows");
         const int kI = p.k_iters, sp = u.split;
         const int first = sk_owner(p, sp * kI), last = sk_owner(p, sp * kI + kI - 1);
         wait_vmcnt<0>();
@@ -1264,7 +1404,7 @@ struct Engine {
     }
     template <int EPI, int WK>
     __device__ __forceinline__ void finish_piece_sliced_as(const GemmParams& p, const Unit& u, int v,
-                                                           uint32_t slot_off, bool next, f32x16 (&acc)[FN][FM]) {
+                                                           uint32_t slot_off, bool next, Acc (&acc)[FN][FM]) {
         if (next) wait_vmcnt<PRO_LOADS>();
         else wait_vmcnt<0>();
         barrier();
@@ -1280,7 +1420,7 @@ struct Engine {
     // blocks it owns.
     template <int EPI>
     __device__ __forceinline__ void finish_split(const GemmParams& p, const Unit& u, int v, bool next,
-                                                 f32x16 (&acc)[FN][FM]) {
+                                                 Acc (&acc)[FN][FM]) {
         const uint32_t slot_off = (uint32_t)((sk_slot(p, v, u.local, C::BM * C::BN) - p.ws) * 4);
         if constexpr (C::WGK > 1) {
             if (wk == 0) finish_piece_sliced_as<EPI, 0>(p, u, v, slot_off, next, acc);
@@ -1305,7 +1445,9 @@ struct Engine {
 // A tile with an early refill stores from registers too: the next unit's DMA prologue then fills
 // part of stage S-1, the staging area.
 template <class C, int EPI, bool SK>
-constexpr bool epi_in_regs() { return EPI != EPI_STORE || SK || !C::OUT_POW2 || C::PROD > 0 || C::EARLY > 0; }
+constexpr bool epi_in_regs() {
+    return EPI != EPI_STORE || SK || !C::OUT_POW2 || C::PROD > 0 || C::EARLY > 0 || C::MF != 32;
+}
 
 // The wave roles of a tile: with refill-only waves (C::PROD > 0) waves [0, PROD) issue the whole
 // refill and hold no wave tile, and the others hold wave tiles and issue no DMA; otherwise every
@@ -1335,7 +1477,7 @@ __device__ __forceinline__ void walk_units(const GemmParams& p, lds_char* smem, 
     // and finish (no barrier), or a K-sliced tile's exchange, whose barriers they pass too
     static_assert(C::PROD == 0 || EPI_IN_REGS || C::WGK > 1, "refill waves: no staged epilogue");
     Engine<DT, C, GATHER, ISSUE, MMA> eng(smem, p);
-    f32x16 acc[C::FN][C::FM];
+    typename AccOf<C::MF>::type acc[C::FN][C::FM];
     UnitWalker<SK> walk(p, v, G);
     Unit u = walk.next(p);
     if (!u.valid) return;

@@ -1,9 +1,10 @@
 // ffn_variants.hpp -- the macro-tile variants compiled into libffn_mi355x.so.
 //
-// X(id, BM, BN, BK, waves along M, waves along N, LDS stages[, sync slot, DMA k-steps,
-//   waves along K, waves issuing the refill, refill-only waves, early refill loads])
-// (DMA k-steps equal to the k-steps per stage spreads a deep pipeline's refill over the
-// whole iteration.)  The K-sliced 128x128 tiles (10, 11) give each wave a 128x64 wave tile
+// X(id, BM, BN, BK, waves along M, waves along N, LDS stages[, sync slot, DMA k-steps (of 16 K),
+//   waves along K, waves issuing the refill, refill-only waves, early refill loads, MFMA block
+//   edge (32: 32x32x16, 16: 16x16x32)])
+// (DMA k-steps covering the whole stage spread a deep pipeline's refill over the whole
+// iteration.)  The K-sliced 128x128 tiles (10, 11) give each wave a 128x64 wave tile
 // over half of every stage: a quarter fewer fragment reads per MFMA than 64x64 wave tiles,
 // for the down GEMMs whose output has about one 128x128 tile per CU.  Variant 13 runs it with
 // eight waves (2x2 along M and N, 64x64 wave tiles), two per SIMD, so one wave's MFMAs cover
@@ -23,6 +24,16 @@
 // SIMD now); decode Basic down -18% (20) while its weights stay in
 // the last-level cache (smoke and decode-shard FFNs; the full decode FFN streams them from HBM
 // at the same rate either way).
+// Variants 22 and 23 take 16x16x32 MFMAs.  Under the DiT-size FFN's load the clock is held
+// down by the chip's activity, and a 16x16x32 MFMA takes about 10% less energy per FLOP than a
+// 32x32x16 one (register-only MFMA streams at 1.35 kW: 675 against 750 J per PFLOP), so the
+// same power buys a higher clock (up GEMM 1826 against 1663 MHz).  Variant 22 is variant 12's
+// 256x256 tile with 64x128 wave tiles (4x2 waves: 12 fragments of 16 rows per k-step instead of
+// 16 for 128x64), its stage barrier at slot 23 of 32 and three quarters of each refill issued
+// early, the rest in the first quarter of the iteration: at the higher clock the down GEMM's
+// operands need the longer lead (DiT-size, one interleaved run against variant 12: up 472.5 ->
+// 448.5 us, Stream-K down 464.1 -> 445.9 us, whole FFN 953.6 -> 918.2 us).  Variant 23 is
+// variant 17 with 16x16x32 blocks.
 // The deep-pipeline 64-row tiles (8, 9) keep 56 KiB or more of weights in flight per CU for
 // the memory-bound small-M (decode) shapes.  Variant 14 K-slices the 64x64 tile (64x32 wave
 // tiles over half of every stage): two MFMAs per k-step per wave instead of one, for the
@@ -57,9 +68,11 @@
     X(18, 128, 128, 64, 2, 2, 4, 3, 2, 2, 0, 4)  \
     X(19, 64, 64, 128, 1, 2, 5, -1, 4, 2, 0, 4)  \
     X(20, 32, 32, 128, 1, 1, 8, -1, 4, 2, 0, 2)  \
-    X(21, 128, 128, 64, 1, 2, 4, -1, 2, 2, 0, 4)
+    X(21, 128, 128, 64, 1, 2, 4, -1, 2, 2, 0, 4) \
+    X(22, 256, 256, 64, 4, 2, 2, 23, 1, 1, 4, 0, 12, 16) \
+    X(23, 256, 128, 64, 2, 2, 3, -1, 4, 1, 0, 4, 0, 16)
 
-#define FFN_NUM_VARIANTS 22
+#define FFN_NUM_VARIANTS 24
 
 // (up variant, down variant) pairs compiled as a single-launch FFN (ffn_fused.hip); the two tiles
 // of a pair have the same number of waves, and the up tile's rows are whole down tile rows.  The

@@ -245,6 +245,12 @@ int ffn_mi355x_variant_info(int variant, int* bm, int* bn, int* bk, int* waves, 
  * tile table for planners and tests. */
 int ffn_mi355x_variant_refill_waves(int variant);
 
+/* MFMA block edge of a tile variant: 32 (v_mfma_f32_32x32x16) or 16 (v_mfma_f32_16x16x32), or a
+ * negative code for a variant out of range.  No counterpart in the reference (its tiles are
+ * fixed, ops/host/tiling.py:11-25): tiles of the two edges sum each output in a different
+ * order, so only tiles of one edge compute bit-identical results. */
+int ffn_mi355x_variant_mfma_edge(int variant);
+
 /* Message of the last failure on this thread ("" if none). */
 const char* ffn_mi355x_last_error(void);
 

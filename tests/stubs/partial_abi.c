@@ -65,6 +65,8 @@ int ffn_mi355x_variant_info(int variant, int* bm, int* bn, int* bk, int* waves, 
 
 int ffn_mi355x_variant_refill_waves(int variant) { return variant == 0 ? 0 : FFN_MI355X_EINVAL; }
 
+int ffn_mi355x_variant_mfma_edge(int variant) { return variant == 0 ? 32 : FFN_MI355X_EINVAL; }
+
 const char* ffn_mi355x_last_error(void) { return ""; }
 
 const char* ffn_mi355x_strerror(int code) { return code ? "error" : "ok"; }

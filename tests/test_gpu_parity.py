@@ -415,17 +415,19 @@ def test_every_variant_at_logical_widths(dtype):
 
 
 def _refill_bases():
-    """(refill-wave tile, its base tile): same macro tile, stages and tile waves, no refill
-    waves (the base's waves equal the tile waves of the other)."""
+    """(refill-wave tile, its base tile): same macro tile, stages, MFMA shape and tile waves, no
+    refill waves (the base's waves equal the tile waves of the other).  A refill-wave tile of
+    16x16x32 blocks (23) has no base of its own shape; the all-variant tests cover it."""
     infos = _lib.variants()
     pairs = []
     for v in infos:
         if v["refill_waves"] == 0:
             continue
         base = [b for b in infos if b["refill_waves"] == 0 and b["waves"] == v["waves"] - v["refill_waves"]
-                and all(b[f] == v[f] for f in ("bm", "bn", "bk", "stages"))]
-        assert base, v
-        pairs.append((v["variant"], base[0]["variant"]))
+                and all(b[f] == v[f] for f in ("bm", "bn", "bk", "stages", "mfma_edge"))]
+        assert base or v["mfma_edge"] == 16, v
+        if base:
+            pairs.append((v["variant"], base[0]["variant"]))
     return pairs
 
 

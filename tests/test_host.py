@@ -149,13 +149,25 @@ def test_streamk_schedule_exact_once_and_slots(G):
             assert n.workspace_bytes == counters + Gs * n.down_slots_per_wg * n.down_bm * n.down_bn * 4
 
 
+def test_tiles_report_their_mfma_edge():
+    """Variants 22 and 23 take 16x16x32 MFMAs, every other tile 32x32x16; the query refuses an
+    out-of-range variant."""
+    infos = _lib.variants()
+    assert {v["variant"] for v in infos if v["mfma_edge"] == 16} == {22, 23}
+    assert all(v["mfma_edge"] == 32 for v in infos if v["variant"] not in (22, 23))
+    with pytest.raises(ValueError):
+        _lib.check(_lib.load().ffn_mi355x_variant_mfma_edge(len(infos)))
+    with pytest.raises(ValueError):
+        _lib.check(_lib.load().ffn_mi355x_variant_mfma_edge(-1))
+
+
 def test_refill_wave_tiles_report_their_waves():
     """Tiles whose LDS refill is issued by waves of their own report them and count them in
     their waves; they plan like every other tile (whole, Stream-K and split up GEMMs), and the
     query refuses an out-of-range variant."""
     infos = _lib.variants()
     refill = [v for v in infos if v["refill_waves"] > 0]
-    assert {v["variant"] for v in refill} == {17, 18, 19, 20, 21}
+    assert {v["variant"] for v in refill} == {17, 18, 19, 20, 21, 23}
     for v in refill:
         assert v["waves"] > v["refill_waves"] > 0
         # decode down: 16 rows, 5120 wide, 13824 deep -- every tile count leaves a remainder
@@ -619,12 +631,12 @@ def test_compile_kernel_binds_a_plan_without_a_device():
 # The tile each measured workload runs on, as the design notes' tile table states it:
 # (case id, down path) -> (up variant, down variant).
 TUNED_ASSIGNMENTS = {
-    ("c5_dit_bf16", "basic"): (12, 17), ("c5_dit_bf16", "streamk"): (12, 12),
-    ("c2_aligned_bf16", "basic"): (12, 21), ("c2_aligned_bf16", "streamk"): (12, 17),
+    ("c5_dit_bf16", "basic"): (22, 23), ("c5_dit_bf16", "streamk"): (22, 22),
+    ("c2_aligned_bf16", "basic"): (22, 21), ("c2_aligned_bf16", "streamk"): (22, 23),
     ("c3_unaligned_fp16", "basic"): (18, 19), ("c3_unaligned_fp16", "streamk"): (18, 5),
     ("c4_decode_bf16", "basic"): (8, 20), ("c4_decode_bf16", "streamk"): (8, 19),
     ("c1_smoke_fp16", "basic"): (4, 20), ("c1_smoke_fp16", "streamk"): (4, 20),
-    ("c5_tp8_shard_bf16", "basic"): (12, 17), ("c5_tp8_shard_bf16", "streamk"): (12, 12),
+    ("c5_tp8_shard_bf16", "basic"): (22, 23), ("c5_tp8_shard_bf16", "streamk"): (22, 22),
     ("c4_tp8_shard_bf16", "basic"): (15, 20), ("c4_tp8_shard_bf16", "streamk"): (19, 19),
 }
 

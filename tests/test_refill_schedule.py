@@ -29,8 +29,8 @@ from pathlib import Path
 import pytest
 
 CSRC = Path(__file__).resolve().parent.parent / "ffn_optim_amd" / "csrc"
-NAMES = ("bm", "bn", "bk", "wgm", "wgn", "stages", "syncq", "dmaks", "wgk", "dmaw", "prod", "early")
-DEFAULTS = dict(syncq=-1, dmaks=-1, wgk=1, dmaw=0, prod=0, early=0)
+NAMES = ("bm", "bn", "bk", "wgm", "wgn", "stages", "syncq", "dmaks", "wgk", "dmaw", "prod", "early", "mf")
+DEFAULTS = dict(syncq=-1, dmaks=-1, wgk=1, dmaw=0, prod=0, early=0, mf=32)
 
 
 def tiles() -> dict[int, dict]:
@@ -51,19 +51,22 @@ def derived(c: dict) -> dict:
     """TileCfg's and Engine's compile-time constants (ffn_gemm.hpp)."""
     c = dict(c)
     nw = c["wgm"] * c["wgn"] * c["wgk"]
-    c["FM"], c["FN"] = c["bm"] // c["wgm"] // 32, c["bn"] // c["wgn"] // 32
+    mf = c["mf"]
+    c["FM"], c["FN"] = c["bm"] // c["wgm"] // mf, c["bn"] // c["wgn"] // mf
     c["NM"] = c["FM"] * c["FN"]
-    c["KS"] = c["bk"] // 16 // c["wgk"]
+    c["KS"] = c["bk"] // (512 // mf) // c["wgk"]
+    c["SPLIT"] = mf == 16
     c["S"] = c["stages"]
     dw = c["prod"] if c["prod"] > 0 else (nw if c["dmaw"] == 0 else c["dmaw"])
     rowb = c["bk"] * 2
     a_blks, b_blks = c["bm"] * rowb // 1024, c["bn"] * rowb // 1024
     c["LOADS"] = a_blks // dw + b_blks // dw
-    c["SYNC_Q"] = c["syncq"] if c["syncq"] >= 0 else c["FM"] - 1
+    c["SYNC_Q"] = c["syncq"] if c["syncq"] >= 0 else (c["NM"] // 2 - 1 if c["SPLIT"] else c["FM"] - 1)
+    c["PRO_Q"] = c["NM"] - 1 if c["SPLIT"] else c["SYNC_Q"]
     S, KS, NM = c["S"], c["KS"], c["NM"]
-    c["DMA_ALL"] = S > 2 and c["dmaks"] == KS
+    c["DMA_ALL"] = S > 2 and c["dmaks"] * 16 == KS * (512 // mf)
     if S == 2:
-        c["DMA_SLOTS"] = (c["dmaks"] if c["dmaks"] > 0 else KS // 2) * NM
+        c["DMA_SLOTS"] = c["dmaks"] * NM * 16 // (512 // mf) if c["dmaks"] > 0 else KS // 2 * NM
     elif c["DMA_ALL"]:
         c["DMA_SLOTS"] = KS * NM
     else:
@@ -111,31 +114,50 @@ def run_units(c: dict, units: list[int], mutation: str | None = None) -> Wave:
         mode = 0 if ksi + 1 < KS else (2 if last else 1)
         nxt = (cur + 1) % S
         half = NM // 2 if NM // 2 > 0 else 1
+        split, hs, fmh = c["SPLIT"], NM // 2, FM // 2
+        # split order (16x16 blocks): the last slot of a k-step using each A / B fragment
+        last_use = ([(i // fmh) * hs + (FN - 1) * fmh + i % fmh for i in range(FM)]
+                    + [hs + j * fmh + fmh - 1 for j in range(FN)]) if split else []
         for q in range(NM):
             j, i = q // FM, q % FM
             # (the MFMA of slot q uses registers only)
-            if mode == 0:
+            if mode == 0 and split:
+                for lu in last_use:
+                    if lu == q:
+                        w.read(cur, (u, it))
+            elif mode == 0:
                 a0, a1 = q * FM // half, min((q + 1) * FM // half, FM)
                 if q < half and a1 > a0:
                     w.read(cur, (u, it))
                 if i == FM - 1:
                     w.read(cur, (u, it))
             else:
-                if q == SYNC_Q:
-                    if mode == 1:
-                        w.wait(0 if S == 2 else c["STAGE_WAIT"])
-                        w.barrier()
-                    elif u + 1 < len(units):
-                        w.barrier()
-                        prologue(u + 1)
+                if mode == 1 and q == SYNC_Q:
+                    w.wait(0 if S == 2 else c["STAGE_WAIT"])
+                    w.barrier()
+                elif mode == 2 and q == c["PRO_Q"] and u + 1 < len(units):
+                    w.barrier()
+                    prologue(u + 1)
+                if mode == 1 and q < SYNC_Q and split and mutation == "split_next_stage_before_barrier":
+                    # the planted mistake: a fragment freed before the stage barrier read from the
+                    # next stage at once
+                    for lu in last_use:
+                        if lu == q:
+                            w.read(nxt, (u, it + 1))
                 if mode == 1 and q >= SYNC_Q:
                     span, qq = NM - SYNC_Q, q - SYNC_Q
-                    a0, a1 = qq * FM // span, (qq + 1) * FM // span
-                    if a1 > a0:
-                        w.read(nxt, (u, it + 1))
-                    for jj in range(FN):
-                        if max(jj * FM + FM - 1, SYNC_Q) == q:
+                    if split:
+                        for lu in last_use:
+                            if max(lu, SYNC_Q) == q and not (mutation == "split_next_stage_before_barrier"
+                                                             and lu < SYNC_Q):
+                                w.read(nxt, (u, it + 1))
+                    else:
+                        a0, a1 = qq * FM // span, (qq + 1) * FM // span
+                        if a1 > a0:
                             w.read(nxt, (u, it + 1))
+                        for jj in range(FN):
+                            if max(jj * FM + FM - 1, SYNC_Q) == q:
+                                w.read(nxt, (u, it + 1))
                     if EARLY and not last and mutation != "early_before_barrier":
                         e0, e1 = qq * EARLY // span, (qq + 1) * EARLY // span
                         stage = nxt if mutation == "early_into_next_stage" else cur
@@ -238,3 +260,17 @@ def test_planted_mistakes_in_the_early_refill_are_caught(mutation):
     for v in early_tiles():
         c = tiles()[v]
         assert any(violations(c, run_units(c, units, mutation)) for units in UNIT_SHAPES), (v, mutation)
+
+
+def split_tiles():
+    return [v for v, c in tiles().items() if c["SPLIT"]]
+
+
+def test_planted_mistake_in_the_split_order_is_caught():
+    """16x16 tiles read a fragment freed before the stage barrier only after it: reading the next
+    stage at once breaks the read-after-refill rule."""
+    assert split_tiles(), "no compiled tile takes 16x16x32 blocks"
+    for v in split_tiles():
+        c = tiles()[v]
+        assert any(violations(c, run_units(c, units, "split_next_stage_before_barrier"))
+                   for units in UNIT_SHAPES), v
