@@ -185,7 +185,6 @@ struct TileCfg {
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
     static_assert(ROWB % 16 == 0 && CH >= 2, "BK must be a multiple of 16");
     static_assert(BK % (KSTEP_K * WGK) == 0, "every wave takes whole k-steps of a stage");
-    static_assert(MF == 32 || WGK == 1, "16x16x32 blocks: no K slices (their exchange moves 32x32 blocks)");
     static_assert(NW % DW == 0 && A_BLKS % DW == 0 && B_BLKS % DW == 0,
                   "DMA blocks must split evenly over the issuing waves");
     static_assert(MF % (CH * R256) == 0, "fragment rows start on a swizzle period");
@@ -475,8 +474,8 @@ struct UnitWalker {
 template <int DT, class C, bool GA, bool ISSUE, bool MMA>
 struct Engine {
     static constexpr int FM = C::FM, FN = C::FN, NT = C::NT, S = C::STAGES, KS = C::KSTEPS;
-    static_assert(KS % 2 == 0, "fragment double-buffer assumes an even number of k-steps per wave");
     static constexpr int MF = C::MF;
+    static_assert(MF == 16 || KS % 2 == 0, "fragment double-buffer assumes an even number of k-steps per wave");
     using Acc = typename AccOf<MF>::type;
     static constexpr int NQ = MF == 32 ? 4 : 1;  // groups of four accumulators per block
     static constexpr int CPK = C::KSTEP_K / 8;   // 16-byte K chunks of one k-step (2 or 4)
@@ -1199,7 +1198,7 @@ struct Engine {
     // The two slices of a wave tile hold FP32 partial sums over the two halves of every stage.
     // Slice WK owns row blocks [WK*IH, (WK+1)*IH) (all j).  Each slice writes the blocks its
     // partner owns into the free stage(s) in register order -- 16-byte group q of block b at
-    // ((b*4 + q)*64 + lane)*16 of the wave's area, so every ds_write_b128 / ds_read_b128 is one
+    // ((b*NQ + q)*64 + lane)*16 of the wave's area, so every ds_write_b128 / ds_read_b128 is one
     // contiguous 1 KiB -- the partner adds them to its own, and each slice then activates,
     // casts and stores its blocks from registers.  A sum of two FP32 terms does not depend on
     // which slice adds, so the result is bit-reproducible.  The exchange goes in phases of XB
@@ -1210,7 +1209,8 @@ struct Engine {
     static constexpr int own_base(int wk) { return wk == 0 ? 0 : OWN0; }
     static constexpr int XMAX = FN * (OWN0 > FM - OWN0 ? OWN0 : FM - OWN0);  // most blocks a wave sends
     static constexpr int XPW = C::EPI_AVAIL / C::NW;      // exchange bytes per wave
-    static constexpr int XB = XPW / 4096 < XMAX ? XPW / 4096 : XMAX;  // blocks per phase
+    static constexpr int XBLK = NQ * 1024;                // exchange bytes of one block
+    static constexpr int XB = XPW / XBLK < XMAX ? XPW / XBLK : XMAX;  // blocks per phase
     static_assert(C::WGK == 1 || (C::WGK == 2 && XB >= 1),
                   "K slicing: two slices, room for one block per wave");
 
@@ -1221,8 +1221,8 @@ struct Engine {
         if constexpr (B0 < B1) {
             constexpr int j = B0 / ROWS, i = BASE + B0 % ROWS, sl = B0 % XB;
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                *(__attribute__((address_space(3))) f32x4*)(area + ((sl * 4 + q) * 64 + lane) * 16) =
+            for (int q = 0; q < NQ; ++q)
+                *(__attribute__((address_space(3))) f32x4*)(area + ((sl * NQ + q) * 64 + lane) * 16) =
                     f32x4{acc[j][i][4 * q], acc[j][i][4 * q + 1], acc[j][i][4 * q + 2], acc[j][i][4 * q + 3]};
             xsend<ROWS, BASE, B0 + 1, B1>(area, acc);
         }
@@ -1232,8 +1232,8 @@ struct Engine {
         if constexpr (B0 < B1) {
             constexpr int j = B0 / ROWS, i = BASE + B0 % ROWS, sl = B0 % XB;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const f32x4 v = *(const __attribute__((address_space(3))) f32x4*)(area + ((sl * 4 + q) * 64 + lane) * 16);
+            for (int q = 0; q < NQ; ++q) {
+                const f32x4 v = *(const __attribute__((address_space(3))) f32x4*)(area + ((sl * NQ + q) * 64 + lane) * 16);
 #pragma unroll
                 for (int c = 0; c < 4; ++c) acc[j][i][4 * q + c] += v[c];
             }

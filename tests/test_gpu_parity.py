@@ -417,7 +417,7 @@ def test_every_variant_at_logical_widths(dtype):
 def _refill_bases():
     """(refill-wave tile, its base tile): same macro tile, stages, MFMA shape and tile waves, no
     refill waves (the base's waves equal the tile waves of the other).  A refill-wave tile of
-    16x16x32 blocks (23) has no base of its own shape; the all-variant tests cover it."""
+    16x16x32 blocks (23, 24) has no base of its own shape; the all-variant tests cover it."""
     infos = _lib.variants()
     pairs = []
     for v in infos:

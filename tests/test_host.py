@@ -150,11 +150,11 @@ def test_streamk_schedule_exact_once_and_slots(G):
 
 
 def test_tiles_report_their_mfma_edge():
-    """Variants 22 and 23 take 16x16x32 MFMAs, every other tile 32x32x16; the query refuses an
+    """Variants 22-24 take 16x16x32 MFMAs, every other tile 32x32x16; the query refuses an
     out-of-range variant."""
     infos = _lib.variants()
-    assert {v["variant"] for v in infos if v["mfma_edge"] == 16} == {22, 23}
-    assert all(v["mfma_edge"] == 32 for v in infos if v["variant"] not in (22, 23))
+    assert {v["variant"] for v in infos if v["mfma_edge"] == 16} == {22, 23, 24}
+    assert all(v["mfma_edge"] == 32 for v in infos if v["variant"] not in (22, 23, 24))
     with pytest.raises(ValueError):
         _lib.check(_lib.load().ffn_mi355x_variant_mfma_edge(len(infos)))
     with pytest.raises(ValueError):
@@ -167,7 +167,7 @@ def test_refill_wave_tiles_report_their_waves():
     query refuses an out-of-range variant."""
     infos = _lib.variants()
     refill = [v for v in infos if v["refill_waves"] > 0]
-    assert {v["variant"] for v in refill} == {17, 18, 19, 20, 21, 23}
+    assert {v["variant"] for v in refill} == {17, 18, 19, 20, 21, 23, 24}
     for v in refill:
         assert v["waves"] > v["refill_waves"] > 0
         # decode down: 16 rows, 5120 wide, 13824 deep -- every tile count leaves a remainder
@@ -477,7 +477,7 @@ def test_k_sliced_variants_plan_for_basic_and_streamk():
     Stream-K form (the slices are summed before a split piece writes its partial)."""
     from ffn_optim_amd import _lib
     ids = _k_sliced_variants()
-    assert {10, 11, 13, 14, 15, 16, 18, 19, 20, 21} == ids
+    assert {10, 11, 13, 14, 15, 16, 18, 19, 20, 21, 24} == ids
     sliced = [v for v in _lib.variants() if v["variant"] in ids]
     for v in sliced:
         assert v["waves"] - v["refill_waves"] in (2, 4, 8) and v["lds_bytes"] <= 160 * 1024
@@ -632,7 +632,7 @@ def test_compile_kernel_binds_a_plan_without_a_device():
 # (case id, down path) -> (up variant, down variant).
 TUNED_ASSIGNMENTS = {
     ("c5_dit_bf16", "basic"): (22, 23), ("c5_dit_bf16", "streamk"): (22, 22),
-    ("c2_aligned_bf16", "basic"): (22, 21), ("c2_aligned_bf16", "streamk"): (22, 23),
+    ("c2_aligned_bf16", "basic"): (22, 24), ("c2_aligned_bf16", "streamk"): (22, 23),
     ("c3_unaligned_fp16", "basic"): (18, 19), ("c3_unaligned_fp16", "streamk"): (18, 5),
     ("c4_decode_bf16", "basic"): (8, 20), ("c4_decode_bf16", "streamk"): (8, 19),
     ("c1_smoke_fp16", "basic"): (4, 20), ("c1_smoke_fp16", "streamk"): (4, 20),
