@@ -24,7 +24,7 @@
 // SIMD now); decode Basic down -18% (20) while its weights stay in
 // the last-level cache (smoke and decode-shard FFNs; the full decode FFN streams them from HBM
 // at the same rate either way).
-// Variants 22-24 take 16x16x32 MFMAs.  Under the DiT-size FFN's load the clock is held
+// Variants 22-25 take 16x16x32 MFMAs.  Under the DiT-size FFN's load the clock is held
 // down by the chip's activity, and a 16x16x32 MFMA takes about 10% less energy per FLOP than a
 // 32x32x16 one (register-only MFMA streams at 1.35 kW: 675 against 750 J per PFLOP), so the
 // same power buys a higher clock (up GEMM 1826 against 1663 MHz).  Variant 22 is variant 12's
@@ -35,7 +35,10 @@
 // 448.5 us, Stream-K down 464.1 -> 445.9 us, whole FFN 953.6 -> 918.2 us).  Variant 23 is
 // variant 17 with 16x16x32 blocks, variant 24 variant 21 (the K-sliced 128x128 tile, its slices
 // exchanging 16x16 blocks): aligned mid-size Basic down 31.8 -> 29.7 us (the 16x16 forms of
-// variants 18 and 19 gained 1% on the unaligned FFN, within the noise: not kept).
+// variants 18 and 19 gained 1% on the unaligned FFN, within the noise: not kept).  Variant 25
+// is a 256x192 tile of 16x16 blocks (64x96 wave tiles, barrier at slot 17 of 24, 10 of 14
+// refill loads early) for the DiT FFN's H/8 shard, whose up GEMM has 192 tiles of 256x256 on 256
+// CUs and 256 of 256x192: shard up 74.5 -> 62.6 us, Basic FFN 137.4 -> 128.5 us.
 // The deep-pipeline 64-row tiles (8, 9) keep 56 KiB or more of weights in flight per CU for
 // the memory-bound small-M (decode) shapes.  Variant 14 K-slices the 64x64 tile (64x32 wave
 // tiles over half of every stage): two MFMAs per k-step per wave instead of one, for the
@@ -73,9 +76,10 @@
     X(21, 128, 128, 64, 1, 2, 4, -1, 2, 2, 0, 4) \
     X(22, 256, 256, 64, 4, 2, 2, 23, 1, 1, 4, 0, 12, 16) \
     X(23, 256, 128, 64, 2, 2, 3, -1, 4, 1, 0, 4, 0, 16) \
-    X(24, 128, 128, 64, 1, 2, 4, -1, 2, 2, 0, 4, 0, 16)
+    X(24, 128, 128, 64, 1, 2, 4, -1, 2, 2, 0, 4, 0, 16) \
+    X(25, 256, 192, 64, 4, 2, 2, 17, 1, 1, 4, 0, 10, 16)
 
-#define FFN_NUM_VARIANTS 25
+#define FFN_NUM_VARIANTS 26
 
 // (up variant, down variant) pairs compiled as a single-launch FFN (ffn_fused.hip); the two tiles
 // of a pair have the same number of waves, and the up tile's rows are whole down tile rows.  The

@@ -75,7 +75,8 @@ def test_swiglu_plans_use_block_pair_tiles():
                            activation="swiglu")
         except ValueError as exc:
             assert "SwiGLU" in str(exc)
-            assert v["bn"] <= 64     # only the narrow tiles lack block pairs
+            # only the narrow tiles and the 256x192 tile (96-column wave tiles) lack block pairs
+            assert v["bn"] <= 64 or v["bn"] % 128 != 0
     # SiLU splits like the GELU: the decode shard's up
     plan = _lib.make_plan(64, 5120, 1728, 5120, code, "basic", "erf", 256, 8, -1, m=16, activation="silu")
     assert plan.up_sk_tiles > 0

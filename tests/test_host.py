@@ -150,11 +150,11 @@ def test_streamk_schedule_exact_once_and_slots(G):
 
 
 def test_tiles_report_their_mfma_edge():
-    """Variants 22-24 take 16x16x32 MFMAs, every other tile 32x32x16; the query refuses an
+    """Variants 22-25 take 16x16x32 MFMAs, every other tile 32x32x16; the query refuses an
     out-of-range variant."""
     infos = _lib.variants()
-    assert {v["variant"] for v in infos if v["mfma_edge"] == 16} == {22, 23, 24}
-    assert all(v["mfma_edge"] == 32 for v in infos if v["variant"] not in (22, 23, 24))
+    assert {v["variant"] for v in infos if v["mfma_edge"] == 16} == {22, 23, 24, 25}
+    assert all(v["mfma_edge"] == 32 for v in infos if v["variant"] not in (22, 23, 24, 25))
     with pytest.raises(ValueError):
         _lib.check(_lib.load().ffn_mi355x_variant_mfma_edge(len(infos)))
     with pytest.raises(ValueError):
@@ -636,7 +636,7 @@ TUNED_ASSIGNMENTS = {
     ("c3_unaligned_fp16", "basic"): (18, 19), ("c3_unaligned_fp16", "streamk"): (18, 5),
     ("c4_decode_bf16", "basic"): (8, 20), ("c4_decode_bf16", "streamk"): (8, 19),
     ("c1_smoke_fp16", "basic"): (4, 20), ("c1_smoke_fp16", "streamk"): (4, 20),
-    ("c5_tp8_shard_bf16", "basic"): (22, 23), ("c5_tp8_shard_bf16", "streamk"): (22, 22),
+    ("c5_tp8_shard_bf16", "basic"): (25, 23), ("c5_tp8_shard_bf16", "streamk"): (25, 22),
     ("c4_tp8_shard_bf16", "basic"): (15, 20), ("c4_tp8_shard_bf16", "streamk"): (19, 19),
 }
 
