@@ -132,6 +132,10 @@ double tile_eff(const Variant& v) {
     const double refill = (v.prod > 0 ? 1.03 : 1.0) * (v.mf == 16 ? 1.05 : 1.0);
     if (v.wgk > 1) return refill * (a >= 128 ? (v.nw >= 8 ? 0.9 : 0.85) : 0.3);
     if (a >= 256) return refill * 1.0;
+    // 256x192 (16x16 blocks): 0.92 per FLOP of the 256x256 tile, from the DiT-size up at eight
+    // tiles per CU (493.5 against 453.0 us at six of 256x256) and its H/8 shard at one wave of
+    // tiles (62.6 against 74.5 us on 192 of 256x256)
+    if (a == 192 && b == 256) return refill * 0.92;
     if (a == 128 && b == 256) return refill * 0.95;
     if (a == 128) return refill * 0.6;
     if (a == 64 && b >= 128) return refill * 0.42;
