@@ -650,6 +650,18 @@ def test_tuned_table_assignments(case_id, down):
     assert (plan.up.variant, plan.down.variant) == TUNED_ASSIGNMENTS[(case_id, down)]
 
 
+def test_cost_model_takes_16x16_tiles_and_the_256x192_tile_where_measured():
+    """Without the tuning table the cost model reaches the measured choices on the DiT-size FFN
+    and its H/8 shard: the 256x256 tile of 16x16 blocks (22) over its 32x32 twin (12) for the
+    full FFN's up (six tiles per CU), the 256x192 tile (25) for the shard's up, whose 192 tiles
+    of 256x256 would leave 64 of 256 CUs idle."""
+    from ffn_optim_amd.cases import get_case
+    full = make_plan(case_problem(get_case("c5_dit_bf16")), Selection("basic", "streamk"), 256, tuned=False)
+    shard = make_plan(case_problem(get_case("c5_tp8_shard_bf16")), Selection("basic", "basic"), 256, tuned=False)
+    assert (full.up.variant, full.down.variant) == (22, 22)
+    assert shard.up.variant == 25 and (shard.up.bm, shard.up.bn) == (256, 192)
+
+
 def test_split_counter_stride_matches_header():
     """The Python mirror of the arrival-counter layout (used by the GPU tests that check which
     counter words a plan leaves zero) is the header's FFN_MI355X_SPLIT_COUNTER_WORDS, a 128-byte
