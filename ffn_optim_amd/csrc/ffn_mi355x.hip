@@ -240,10 +240,17 @@ int pick_basic(long long M, long long m_valid, long long N, long long K, int G) 
     return best;
 }
 
+// The 256x192 tile is not an automatic Stream-K down: it would make Stream-K applicable where
+// every power-of-two tiling divides the grid, and there lost to the Basic down it competes with
+// (8192x4096 -> 8192: 877.9 against 774.7 us), its split form holding more work per workgroup
+// than the whole tiles it replaces.  A forced down_variant still takes it.
+bool sk_candidate(const Variant& v) { return !(v.mf == 16 && v.bn == 192); }
+
 int pick_streamk(long long M, long long m_valid, long long N, long long K, int G) {
     int best = -1;
     double best_cost = 1e300;
     for (int i = 0; i < kNumVariants; ++i) {
+        if (!sk_candidate(kVariants[i])) continue;
         SkShape s;
         if (!sk_shape(kVariants[i], m_valid, N, K, G, s)) continue;
         const double c = cost_streamk(kVariants[i], s, m_valid, N, K);
