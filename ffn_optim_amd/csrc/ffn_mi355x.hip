@@ -120,8 +120,9 @@ constexpr double kUnitOverhead = 2.5e-6;   // s per unit: DMA prologue latency +
 
 // Relative MFMA efficiency of each macro tile (measured on the FFN shapes, 256x256 = 1): the
 // fragment reads per MFMA grow as the wave tile shrinks.  A K-sliced 128x128 tile has 128x64
-// wave tiles (and pays an LDS exchange of half its partials per tile); with eight waves, two
-// per SIMD, one wave's MFMAs cover the other's waits.  The K-sliced 64x64 tile (64x32 wave
+// wave tiles (and pays an LDS exchange of half its partials per tile); with two waves per SIMD
+// (eight tile waves, or four beside four refill waves) one wave's work covers the other's waits.
+// The K-sliced 64x64 tile (64x32 wave
 // tiles, two MFMAs per k-step) is a little ahead of the plain one.  A tile whose refill is
 // issued by waves of its own (no wave tile) keeps its tile waves off the texture unit: 1.6-18%
 // ahead of the same tile without them on the Basic downs and unaligned up it serves.  A tile of
@@ -130,7 +131,7 @@ constexpr double kUnitOverhead = 2.5e-6;   // s per unit: DMA prologue latency +
 double tile_eff(const Variant& v) {
     const int a = v.bm < v.bn ? v.bm : v.bn, b = v.bm < v.bn ? v.bn : v.bm;
     const double refill = (v.prod > 0 ? 1.03 : 1.0) * (v.mf == 16 ? 1.05 : 1.0);
-    if (v.wgk > 1) return refill * (a >= 128 ? (v.nw >= 8 ? 0.9 : 0.85) : 0.3);
+    if (v.wgk > 1) return refill * (a >= 128 ? (v.nw + v.prod >= 8 ? 0.9 : 0.85) : 0.3);
     if (a >= 256) return refill * 1.0;
     // 256x192 (16x16 blocks): 0.92 per FLOP of the 256x256 tile, from the DiT-size up at eight
     // tiles per CU (493.5 against 453.0 us at six of 256x256) and its H/8 shard at one wave of
@@ -148,7 +149,11 @@ double iter_time(const Variant& v, long long rows) {
     const double t_mfma = flops / (kCuMfmaRate * tile_eff(v));
     const double bytes = (double)(rows + v.bn) * v.bk * 2.0;
     const double inflight = (double)(v.stages - 1) * (double)(v.bm + v.bn) * v.bk * 2.0;
-    const double rate = std::min(kCuLoadRate, inflight / kLoadLatency);
+    // refill-only waves take the texture unit's stalls off the tile waves, where the refill
+    // bounds the iteration too: the K-sliced 128x128 tile with them (v24) against the one
+    // without (v10), both load-bound here, took the 3000x1000 -> 4000 -> 1000 fp16 FFN's Basic
+    // down 7% faster
+    const double rate = std::min(kCuLoadRate, inflight / kLoadLatency) * (v.prod > 0 ? 1.03 : 1.0);
     return std::max(t_mfma, bytes / rate);
 }
 
@@ -167,6 +172,7 @@ double cost_basic(const Variant& v, long long M, long long m_valid, long long N,
 
 struct SkShape {
     long long tiles, k_iters, grid, dp, sk, q, r, slots;
+    long long pieces;  // pieces per tile of a reduced grid; 0 when the grid is block_num
 };
 
 // Stream-K grid: block_num workgroups, or fewer when every tile is split (fewer tiles than
@@ -178,12 +184,16 @@ struct SkShape {
 // of 67.5; on the smallest FFN's down (8 tiles), 16 one-iteration pieces per tile measured 24%
 // slower than a separate reduction launch.
 constexpr long long kMaxPieces = 4;
-long long sk_grid(long long tiles, long long k_iters, int G) {
+long long sk_pieces(long long tiles, long long k_iters, int G) {
     const long long pmax = std::min<long long>({(long long)G / std::max<long long>(1, tiles), kMaxPieces, k_iters});
-    if (tiles >= G || pmax < 2) return G;
+    if (tiles >= G || pmax < 2) return 0;
     for (long long p = pmax; p >= 2; --p)
-        if (k_iters % p == 0) return tiles * p;
-    return tiles * pmax;
+        if (k_iters % p == 0) return p;
+    return pmax;
+}
+long long sk_grid(long long tiles, long long k_iters, int G) {
+    const long long p = sk_pieces(tiles, k_iters, G);
+    return p ? tiles * p : G;
 }
 
 // Tiles of a GEMM whose rows [m_valid, M) are zero padding: only tile rows holding data are
@@ -196,7 +206,8 @@ bool counters_fit(long long split_tiles, const Variant& v) { return split_tiles 
 bool sk_shape(const Variant& v, long long m_valid, long long N, long long K, int block_num, SkShape& s) {
     s.tiles = cdiv(m_valid, v.bm) * cdiv(N, v.bn);
     s.k_iters = cdiv(K, v.bk);
-    const long long G = sk_grid(s.tiles, s.k_iters, block_num);
+    s.pieces = sk_pieces(s.tiles, s.k_iters, block_num);
+    const long long G = s.pieces ? s.tiles * s.pieces : block_num;
     s.grid = G;
     s.sk = s.tiles % G;
     s.dp = s.tiles - s.sk;
@@ -214,7 +225,18 @@ double cost_streamk(const Variant& v, const SkShape& s, long long m_valid, long 
     const double it = iter_time(v, rows_in_tile(v, m_valid));
     const long long dp_waves = cdiv(s.dp, G);
     const long long sk_iters = s.q + (s.r ? 1 : 0);
-    double t = it * ((double)dp_waves * s.k_iters + (double)sk_iters) +
+    // Pieces that start at scattered depths of their tiles (a grid of block_num workgroups over
+    // a number of split tiles that does not divide it, so a tile holds a fractional number of
+    // pieces): neighbouring workgroups of an XCD read different K slices at any moment, so no
+    // panel slice is shared in L2 and the split iterations stream at the chip's HBM rate.  On the
+    // 1024x5120 -> 13824 -> 5120 fp16 FFN the 256x128 down's 160 tiles so split (1.6 pieces a
+    // tile) took ~270 us, against ~150 us for 80 tiles of 256x256 in three aligned pieces.
+    // A whole number of pieces a tile keeps their offsets within an iteration of K / pieces.
+    const bool scattered = s.pieces == 0 && s.sk > 0 && (G % s.sk) != 0;
+    double it_split = it;
+    if (scattered)
+        it_split = std::max(it, (double)(rows_in_tile(v, m_valid) + v.bn) * v.bk * 2.0 * (double)G / kHbmRate);
+    double t = it * (double)dp_waves * s.k_iters + it_split * (double)sk_iters +
                kUnitOverhead * (double)(dp_waves + 1);
     // shared split tiles: each piece writes its FP32 partial through to memory and counts in;
     // the last reads the others (several at a time when its waves hold at most two 32x32
@@ -230,12 +252,21 @@ double cost_streamk(const Variant& v, const SkShape& s, long long m_valid, long 
     return std::max(t, hbm);
 }
 
+// A candidate replaces the best so far when it is cheaper by more than 0.1%, or within 0.1% on a
+// tile of higher MFMA efficiency: where the load or HBM term bounds every candidate alike (a
+// load-bound 128x128 down, scattered split pieces), the tile that computes faster wins the tie
+// instead of the lower variant number (aligned mid-size down at 2048 rows: v24 133.3 us, v18
+// 147.7, v10 155.0, one tuning run).
+bool better(double c, const Variant& v, double best_cost, const Variant& best) {
+    return c < best_cost * 0.999 || (c <= best_cost * 1.001 && tile_eff(v) > tile_eff(best));
+}
+
 int pick_basic(long long M, long long m_valid, long long N, long long K, int G) {
     int best = 0;
     double best_cost = 1e300;
     for (int i = 0; i < kNumVariants; ++i) {
         const double c = cost_basic(kVariants[i], M, m_valid, N, K, G);
-        if (c < best_cost * 0.999) best_cost = c, best = i;
+        if (better(c, kVariants[i], best_cost, kVariants[best])) best_cost = c, best = i;
     }
     return best;
 }
@@ -254,7 +285,7 @@ int pick_streamk(long long M, long long m_valid, long long N, long long K, int G
         SkShape s;
         if (!sk_shape(kVariants[i], m_valid, N, K, G, s)) continue;
         const double c = cost_streamk(kVariants[i], s, m_valid, N, K);
-        if (c < best_cost * 0.999) best_cost = c, best = i;
+        if (best < 0 || better(c, kVariants[i], best_cost, kVariants[best])) best_cost = c, best = i;
     }
     return best;
 }
@@ -293,7 +324,7 @@ int pick_up(long long M, long long m_valid, long long N, long long K, int G, boo
         const double c = !swiglu && split_up(kVariants[i], m_valid, N, K, G, s)
                              ? cost_streamk(kVariants[i], s, m_valid, N, K)
                              : cost_basic(kVariants[i], M, m_valid, N, K, G);
-        if (c < best_cost * 0.999) best_cost = c, best = i;
+        if (best < 0 || better(c, kVariants[i], best_cost, kVariants[best])) best_cost = c, best = i;
     }
     return best;
 }

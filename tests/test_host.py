@@ -662,6 +662,54 @@ def test_cost_model_takes_16x16_tiles_and_the_256x192_tile_where_measured():
     assert shard.up.variant == 25 and (shard.up.bm, shard.up.bn) == (256, 192)
 
 
+def _untuned(m, k, h, down):
+    p = problem_from_shapes((m, k), (h, k), (k, h), "bfloat16")
+    return make_plan(p, Selection("basic", down), 256, tuned=False)
+
+
+@pytest.mark.parametrize("m, k, h, up, down", [
+    (1024, 5120, 13632, 22, 22),   # was 256x128: 160 tiles, 1.6 pieces a tile (now 28% faster)
+    (3000, 1152, 4608, 22, 23),    # was 128x128: 216 tiles, 1.19 pieces a tile (now 36% faster)
+    (1024, 3072, 12288, 25, 23),   # was 128x128: 192 tiles, 1.33 pieces a tile (now 20% faster)
+])
+def test_cost_model_keeps_stream_k_pieces_aligned(m, k, h, up, down):
+    """A Stream-K down whose split tiles do not divide the grid has pieces starting at scattered
+    depths of their tiles; the model streams those at the HBM rate, so the planner takes a tiling
+    whose split tiles hold a whole number of pieces (every case measured faster than the plan
+    chosen before, interleaved on the same inputs)."""
+    plan = _untuned(m, k, h, "streamk")
+    s = plan.schedule()
+    assert (plan.up.variant, plan.down.variant) == (up, down)
+    assert s["down_sk_tiles"] > 0 and s["down_grid"] % s["down_sk_tiles"] == 0, s
+
+
+def test_forced_scattered_split_still_plans():
+    """The scattered-pieces rule prices a tiling, it does not refuse it: a forced 256x128 down
+    splits its 160 tiles over 256 workgroups as before.  The DiT-size FFN's automatic Stream-K
+    down keeps split tiles that divide its grid (two pieces a tile)."""
+    p = problem_from_shapes((1024, 5120), (13632, 5120), (5120, 13632), "bfloat16")
+    forced = make_plan(p, Selection("basic", "streamk"), 256, up_variant=22, down_variant=23)
+    s = forced.schedule()
+    assert s["down_sk_tiles"] == 160 and s["down_grid"] == 256
+    from ffn_optim_amd.cases import get_case
+    full = make_plan(case_problem(get_case("c5_dit_bf16")), Selection("basic", "streamk"), 256, tuned=False)
+    fs = full.schedule()
+    assert fs["down_grid"] % fs["down_sk_tiles"] == 0
+
+
+@pytest.mark.parametrize("m, k, h, down, up_v, down_v", [
+    (2048, 2048, 8192, "basic", 22, 24),   # load-bound K-sliced downs tie: v24 over v18 and v10
+    (1000, 1024, 4096, "basic", 24, 19),   # the same tie on the up (measured -8%)
+    (16, 3072, 12288, "basic", 20, 20),    # decode tiles with refill waves (measured -12%)
+])
+def test_cost_model_ties_go_to_the_faster_tile(m, k, h, down, up_v, down_v):
+    """Where the load term bounds several tiles alike, a tile with refill-only waves is credited
+    on its load rate too, and a tie goes to the tile of higher MFMA efficiency rather than the
+    lower variant number."""
+    plan = _untuned(m, k, h, down)
+    assert (plan.up.variant, plan.down.variant) == (up_v, down_v)
+
+
 def test_split_counter_stride_matches_header():
     """The Python mirror of the arrival-counter layout (used by the GPU tests that check which
     counter words a plan leaves zero) is the header's FFN_MI355X_SPLIT_COUNTER_WORDS, a 128-byte
