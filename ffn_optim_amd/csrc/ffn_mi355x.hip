@@ -315,15 +315,25 @@ bool split_up(const Variant& v, long long m_valid, long long N, long long K, int
 // needs wave tiles of whole block pairs, and is never split: no split role is compiled for it.
 bool swiglu_tile(const Variant& v) { return (v.bn / v.wgn) % 64 == 0; }
 
+// A tile that would be split competes only when no tiling of 64x64 or more fills more than half
+// of the grid with whole tiles: at 128 rows (128 x 4096 -> 16384) the 128x128 tile split in two
+// pieces priced ahead of 256 whole 64x128 tiles and measured 9-15% slower on the FFN; at 64 rows
+// and H 8192 only the 32x32 decode tiles fill the grid, and the split 64x64 tile stays 10%
+// ahead of them.
 int pick_up(long long M, long long m_valid, long long N, long long K, int G, bool swiglu) {
     int best = -1;
     double best_cost = 1e300;
+    bool fills = false;
+    for (int i = 0; i < kNumVariants; ++i)
+        fills |= (!swiglu || swiglu_tile(kVariants[i])) && kVariants[i].bm * kVariants[i].bn >= 64 * 64 &&
+                 cdiv(m_valid, kVariants[i].bm) * cdiv(N, kVariants[i].bn) * 2 > G;
     for (int i = 0; i < kNumVariants; ++i) {
         if (swiglu && !swiglu_tile(kVariants[i])) continue;
         SkShape s;
-        const double c = !swiglu && split_up(kVariants[i], m_valid, N, K, G, s)
-                             ? cost_streamk(kVariants[i], s, m_valid, N, K)
-                             : cost_basic(kVariants[i], M, m_valid, N, K, G);
+        const bool split = !swiglu && split_up(kVariants[i], m_valid, N, K, G, s);
+        if (split && fills) continue;
+        const double c = split ? cost_streamk(kVariants[i], s, m_valid, N, K)
+                               : cost_basic(kVariants[i], M, m_valid, N, K, G);
         if (best < 0 || better(c, kVariants[i], best_cost, kVariants[best])) best_cost = c, best = i;
     }
     return best;

@@ -697,6 +697,19 @@ def test_forced_scattered_split_still_plans():
     assert fs["down_grid"] % fs["down_sk_tiles"] == 0
 
 
+@pytest.mark.parametrize("m, k, h, up_v, split", [
+    (128, 4096, 16384, 5, False),   # 256 whole 64x128 tiles fill the grid: no split (measured -9%)
+    (256, 2048, 8192, 5, False),    # the same at 256 rows (measured -17%)
+    (64, 2048, 8192, 19, True),     # only 32x32 tiles fill it: the split 64x64 tile stays ahead
+    (16, 5120, 1728, 20, True),     # decode shard: every tiling leaves half the grid idle
+])
+def test_split_up_only_where_no_tiling_fills_the_grid(m, k, h, up_v, split):
+    """The automatic up GEMM is split along K only when no tiling of 64x64 or more would give more
+    than half of the workgroups a whole tile; a forced variant still splits by its own tile count."""
+    plan = _untuned(m, k, h, "basic")
+    assert plan.up.variant == up_v and (plan.native.up_sk_tiles > 0) == split
+
+
 @pytest.mark.parametrize("m, k, h, down, up_v, down_v", [
     (2048, 2048, 8192, "basic", 22, 24),   # load-bound K-sliced downs tie: v24 over v18 and v10
     (1000, 1024, 4096, "basic", 24, 19),   # the same tie on the up (measured -8%)
