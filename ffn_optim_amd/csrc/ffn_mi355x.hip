@@ -131,7 +131,10 @@ constexpr double kUnitOverhead = 2.5e-6;   // s per unit: DMA prologue latency +
 double tile_eff(const Variant& v) {
     const int a = v.bm < v.bn ? v.bm : v.bn, b = v.bm < v.bn ? v.bn : v.bm;
     const double refill = (v.prod > 0 ? 1.03 : 1.0) * (v.mf == 16 ? 1.05 : 1.0);
-    if (v.wgk > 1) return refill * (a >= 128 ? (v.nw + v.prod >= 8 ? 0.9 : 0.85) : 0.3);
+    // The K-sliced 32x32 decode tile (32x32 wave tiles, one MFMA per k-step and wave) reads the
+    // most fragments per MFMA: 0.15, from the 512x1024 -> 4096 -> 1024 FFN's Basic down, where its
+    // 512 tiles took 30.7 us against 27.0 us for 128 K-sliced 64x64 tiles (one tuning run).
+    if (v.wgk > 1) return refill * (a >= 128 ? (v.nw + v.prod >= 8 ? 0.9 : 0.85) : a >= 64 ? 0.3 : 0.15);
     if (a >= 256) return refill * 1.0;
     // 256x192 (16x16 blocks): 0.92 per FLOP of the 256x256 tile, from the DiT-size up at eight
     // tiles per CU (493.5 against 453.0 us at six of 256x256) and its H/8 shard at one wave of
@@ -256,9 +259,12 @@ double cost_streamk(const Variant& v, const SkShape& s, long long m_valid, long 
 // tile of higher MFMA efficiency: where the load or HBM term bounds every candidate alike (a
 // load-bound 128x128 down, scattered split pieces), the tile that computes faster wins the tie
 // instead of the lower variant number (aligned mid-size down at 2048 rows: v24 133.3 us, v18
-// 147.7, v10 155.0, one tuning run).
-bool better(double c, const Variant& v, double best_cost, const Variant& best) {
-    return c < best_cost * 0.999 || (c <= best_cost * 1.001 && tile_eff(v) > tile_eff(best));
+// 147.7, v10 155.0, one tuning run).  Not where the tiles are taller than the rows holding data:
+// a decode-size GEMM at the HBM bound gains nothing from a tall tile's efficiency (16 x 8192 ->
+// 21824: the 128x128 tile 4% behind the 32x32 one).
+bool better(double c, const Variant& v, double best_cost, const Variant& best, long long m_valid) {
+    return c < best_cost * 0.999 || (c <= best_cost * 1.001 && v.bm <= m_valid && best.bm <= m_valid &&
+                                     tile_eff(v) > tile_eff(best));
 }
 
 int pick_basic(long long M, long long m_valid, long long N, long long K, int G) {
@@ -266,7 +272,7 @@ int pick_basic(long long M, long long m_valid, long long N, long long K, int G) 
     double best_cost = 1e300;
     for (int i = 0; i < kNumVariants; ++i) {
         const double c = cost_basic(kVariants[i], M, m_valid, N, K, G);
-        if (better(c, kVariants[i], best_cost, kVariants[best])) best_cost = c, best = i;
+        if (better(c, kVariants[i], best_cost, kVariants[best], m_valid)) best_cost = c, best = i;
     }
     return best;
 }
@@ -285,7 +291,7 @@ int pick_streamk(long long M, long long m_valid, long long N, long long K, int G
         SkShape s;
         if (!sk_shape(kVariants[i], m_valid, N, K, G, s)) continue;
         const double c = cost_streamk(kVariants[i], s, m_valid, N, K);
-        if (best < 0 || better(c, kVariants[i], best_cost, kVariants[best])) best_cost = c, best = i;
+        if (best < 0 || better(c, kVariants[i], best_cost, kVariants[best], m_valid)) best_cost = c, best = i;
     }
     return best;
 }
@@ -334,7 +340,7 @@ int pick_up(long long M, long long m_valid, long long N, long long K, int G, boo
         if (split && fills) continue;
         const double c = split ? cost_streamk(kVariants[i], s, m_valid, N, K)
                                : cost_basic(kVariants[i], M, m_valid, N, K, G);
-        if (best < 0 || better(c, kVariants[i], best_cost, kVariants[best])) best_cost = c, best = i;
+        if (best < 0 || better(c, kVariants[i], best_cost, kVariants[best], m_valid)) best_cost = c, best = i;
     }
     return best;
 }
