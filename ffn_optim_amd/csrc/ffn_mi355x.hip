@@ -122,12 +122,12 @@ constexpr double kUnitOverhead = 2.5e-6;   // s per unit: DMA prologue latency +
 // fragment reads per MFMA grow as the wave tile shrinks.  A K-sliced 128x128 tile has 128x64
 // wave tiles (and pays an LDS exchange of half its partials per tile); with two waves per SIMD
 // (eight tile waves, or four beside four refill waves) one wave's work covers the other's waits.
-// The K-sliced 64x64 tile (64x32 wave
-// tiles, two MFMAs per k-step) is a little ahead of the plain one.  A tile whose refill is
-// issued by waves of its own (no wave tile) keeps its tile waves off the texture unit: 1.6-18%
-// ahead of the same tile without them on the Basic downs and unaligned up it serves.  A tile of
-// 16x16x32 blocks runs at a higher clock for the same power: the DiT-size up GEMM 7% and its
-// Stream-K down 4% faster than on the same tile of 32x32x16 blocks.
+// The K-sliced 64x64 tile (64x32 wave tiles, two MFMAs per k-step) is a little ahead of the
+// plain one.  A tile whose refill is issued by waves of its own (no wave tile) keeps its tile
+// waves off the texture unit: 1.6-18% ahead of the same tile without them on the Basic downs
+// and unaligned up it serves.  A tile of 16x16x32 blocks runs at a higher clock for the same
+// power: the DiT-size up GEMM 7% and its Stream-K down 4% faster than on the same tile of
+// 32x32x16 blocks.
 double tile_eff(const Variant& v) {
     const int a = v.bm < v.bn ? v.bm : v.bn, b = v.bm < v.bn ? v.bn : v.bm;
     const double refill = (v.prod > 0 ? 1.03 : 1.0) * (v.mf == 16 ? 1.05 : 1.0);
