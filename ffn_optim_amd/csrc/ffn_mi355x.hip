@@ -128,7 +128,7 @@ constexpr double kUnitOverhead = 2.5e-6;   // s per unit: DMA prologue latency +
 // and unaligned up it serves.  A tile of 16x16x32 blocks runs at a higher clock for the same
 // power: the DiT-size up GEMM 7% and its Stream-K down 4% faster than on the same tile of
 // 32x32x16 blocks.
-double tile_eff(const Variant& v) {
+double tile_eff(const Variant& v, bool up = false) {
     const int a = v.bm < v.bn ? v.bm : v.bn, b = v.bm < v.bn ? v.bn : v.bm;
     const double refill = (v.prod > 0 ? 1.03 : 1.0) * (v.mf == 16 ? 1.05 : 1.0);
     // The K-sliced 32x32 decode tile (32x32 wave tiles, one MFMA per k-step and wave) reads the
@@ -140,16 +140,21 @@ double tile_eff(const Variant& v) {
     // tiles per CU (493.5 against 453.0 us at six of 256x256) and its H/8 shard at one wave of
     // tiles (62.6 against 74.5 us on 192 of 256x256)
     if (a == 192 && b == 256) return refill * 0.92;
-    if (a == 128 && b == 256) return refill * 0.95;
+    // The 256x128 and 128x256 tiles as the up GEMM (GELU epilogue, short K): 0.88.  On
+    // 16384x1152 -> 4608, 4096x8192 -> 21824 and 8192x1024 -> 2752 the automatic up on the
+    // 256x128 tile ran 2-6% behind the 256x192 or 256x256 tile that a rating of 0.88 picks; as
+    // the down GEMM it keeps 0.95, where the same change lost 5-9% (512x4096 -> 16384 Stream-K,
+    // 4096x5120 -> 13632 Basic).
+    if (a == 128 && b == 256) return refill * (up ? 0.88 : 0.95);
     if (a == 128) return refill * 0.6;
     if (a == 64 && b >= 128) return refill * 0.42;
     return refill * 0.25;
 }
 
 // Seconds per BK-deep iteration of one workgroup on a tile with `rows` data-bearing rows.
-double iter_time(const Variant& v, long long rows) {
+double iter_time(const Variant& v, long long rows, bool up = false) {
     const double flops = 2.0 * v.bm * v.bn * v.bk;
-    const double t_mfma = flops / (kCuMfmaRate * tile_eff(v));
+    const double t_mfma = flops / (kCuMfmaRate * tile_eff(v, up));
     const double bytes = (double)(rows + v.bn) * v.bk * 2.0;
     const double inflight = (double)(v.stages - 1) * (double)(v.bm + v.bn) * v.bk * 2.0;
     // refill-only waves take the texture unit's stalls off the tile waves, where the refill
@@ -163,11 +168,12 @@ double iter_time(const Variant& v, long long rows) {
 long long rows_in_tile(const Variant& v, long long m_valid) { return std::min<long long>(v.bm, m_valid); }
 
 // Estimated seconds of a data-parallel GEMM [M x N] (m_valid data rows), depth K.
-double cost_basic(const Variant& v, long long M, long long m_valid, long long N, long long K, int G) {
+double cost_basic(const Variant& v, long long M, long long m_valid, long long N, long long K, int G,
+                  bool up = false) {
     (void)M;
     const long long T = cdiv(m_valid, v.bm) * cdiv(N, v.bn);
     const long long waves = cdiv(T, G);
-    const double t = (double)waves * ((double)cdiv(K, v.bk) * iter_time(v, rows_in_tile(v, m_valid)) +
+    const double t = (double)waves * ((double)cdiv(K, v.bk) * iter_time(v, rows_in_tile(v, m_valid), up) +
                                       kUnitOverhead);
     const double hbm = (double)(N * K + m_valid * K) * 2.0 / kHbmRate;
     return std::max(t, hbm);
@@ -223,9 +229,10 @@ bool sk_shape(const Variant& v, long long m_valid, long long N, long long K, int
     return s.sk > 0 && s.k_iters >= 2 && counters_fit(s.sk, v);
 }
 
-double cost_streamk(const Variant& v, const SkShape& s, long long m_valid, long long N, long long K) {
+double cost_streamk(const Variant& v, const SkShape& s, long long m_valid, long long N, long long K,
+                    bool up = false) {
     const long long G = s.grid;
-    const double it = iter_time(v, rows_in_tile(v, m_valid));
+    const double it = iter_time(v, rows_in_tile(v, m_valid), up);
     const long long dp_waves = cdiv(s.dp, G);
     const long long sk_iters = s.q + (s.r ? 1 : 0);
     // Pieces that start at scattered depths of their tiles (a grid of block_num workgroups over
@@ -338,8 +345,8 @@ int pick_up(long long M, long long m_valid, long long N, long long K, int G, boo
         SkShape s;
         const bool split = !swiglu && split_up(kVariants[i], m_valid, N, K, G, s);
         if (split && fills) continue;
-        const double c = split ? cost_streamk(kVariants[i], s, m_valid, N, K)
-                               : cost_basic(kVariants[i], M, m_valid, N, K, G);
+        const double c = split ? cost_streamk(kVariants[i], s, m_valid, N, K, true)
+                               : cost_basic(kVariants[i], M, m_valid, N, K, G, true);
         if (best < 0 || better(c, kVariants[i], best_cost, kVariants[best], m_valid)) best_cost = c, best = i;
     }
     return best;

@@ -697,6 +697,16 @@ def test_forced_scattered_split_still_plans():
     assert fs["down_grid"] % fs["down_sk_tiles"] == 0
 
 
+def test_256x128_tile_rated_lower_as_the_up_than_as_the_down():
+    """The 256x128 tile is priced at 0.88 of the 256x256 tile per FLOP as the up GEMM and 0.95 as
+    the down: DiT-XL's up (16384 x 1152 -> 4608) goes to the 256x192 tile (measured 4% faster),
+    while a down it serves well keeps it (4096 x 5120 -> 13632 Basic, where the K-sliced 128x128
+    tile measured 5.5% slower)."""
+    assert _untuned(16384, 1152, 4608, "basic").up.variant == 25
+    assert _untuned(4096, 5120, 13632, "basic").down.variant == 23
+    assert _untuned(8192, 1024, 2752, "basic").up.variant == 25
+
+
 @pytest.mark.parametrize("m, k, h, up_v, split", [
     (128, 4096, 16384, 5, False),   # 256 whole 64x128 tiles fill the grid: no split (measured -9%)
     (256, 2048, 8192, 5, False),    # the same at 256 rows (measured -17%)
